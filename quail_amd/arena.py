@@ -1,0 +1,601 @@
+"""Paged KV arena: page accounting (PageArena) and its device pools (KVArena).
+
+Page accounting follows the reference's rules bit-exactly, since block
+tables and scatter maps are built from it (quail/backends/quail/executor/
+arena.py):
+  - the free list is a stack initialised [n-1, ..., 0]: allocations pop
+    pages 0, 1, 2, ... from a fresh arena, freed pages are pushed back and
+    reused last-in first-out (arena.py:45, :83, :128);
+  - a key's block table is its borrowed pages (a parent's leading pages),
+    then its own (arena.py:115-117);
+  - holds[page] counts the keys holding a page; a page returns to the free
+    list when the count reaches zero (arena.py:122-130);
+  - arena row of (page, slot) is page * page_tokens + slot (arena.py:519-523);
+  - block tables are zero-padded to the widest row (arena.py:874-887).
+
+The device pools use the MI355X layout of quail_amd.layout (K pages
+[n_kv, page, d], V pages transposed [n_kv, d, page]) with the same row
+numbering. Sliding-window pools (DiffusionGemma) are not part of this
+build: an arena asked for one raises.
+"""
+
+import heapq
+
+import numpy as np
+
+from quail_amd import layout
+
+_answer_sink = None
+
+
+def set_answer_sink(sink):
+    """Install the callable evict events go to (quail/progress.py:70-86)."""
+    global _answer_sink
+    _answer_sink = sink
+
+
+def answer_sink():
+    return _answer_sink
+
+
+class PageArena:
+    """Page accounting: a free-page stack and per-key page lists.
+
+    A key may borrow the leading pages of a resident key's prefix; it reads
+    them and never writes them (arena.py:34-40).
+    """
+
+    def __init__(self, n_pages: int, page_tokens: int):
+        self.n_pages = n_pages
+        self.page_tokens = page_tokens
+        self.free = list(range(n_pages - 1, -1, -1))  # stack: pop() -> 0 first
+        self.owned = {}        # key -> pages the key alone writes
+        self.borrowed = {}     # key -> leading pages read from a parent
+        self.holds = [0] * n_pages
+        self.tokens = {}       # key -> resident tokens (borrowed included)
+        self.pinned = set()
+        self.retained = {}     # key -> reusable prefix tokens
+        self._retained_sizes = {}
+        self._retained_pages = 0
+        self._retained_heap = []
+        self._retained_versions = {}
+        self._retention_version = 0
+        self.retention_policy = None
+        self.retention_cap_pages = None
+
+    def pages_needed(self, tokens: int) -> int:
+        return -(-tokens // self.page_tokens)
+
+    def alloc(self, key, tokens: int, capacity_tokens=None, borrowed=()):
+        """Own pages for a fresh key, or None when the free stack is short."""
+        if key in self.owned:
+            raise KeyError(f"{key!r} already resident")
+        capacity = tokens if capacity_tokens is None else capacity_tokens
+        if capacity < tokens:
+            raise ValueError("capacity_tokens must cover logical tokens")
+        borrowed = list(borrowed)
+        if len(borrowed) * self.page_tokens > tokens:
+            raise ValueError("a key cannot borrow past its own tokens")
+        need = self.pages_needed(capacity) - len(borrowed)
+        if need > len(self.free):
+            return None
+        pages = [self.free.pop() for _ in range(need)]
+        self.owned[key] = pages
+        self.borrowed[key] = borrowed
+        self.tokens[key] = tokens
+        for page in borrowed:
+            self.holds[page] += 1
+        for page in pages:
+            self.holds[page] += 1
+        return pages
+
+    def shared_pages(self, parent, shared: int, start: int = 0) -> list:
+        """The parent's pages for its tokens [start, shared), whole pages."""
+        if (shared - start) % self.page_tokens or start % self.page_tokens:
+            raise ValueError("a borrowed prefix is a whole number of pages")
+        if parent not in self.owned:
+            raise KeyError(f"borrow parent {parent!r} is not resident")
+        if shared > self.tokens[parent]:
+            raise ValueError(f"{parent!r} holds fewer tokens than borrowed")
+        first = start // self.page_tokens
+        return self.table_pages(parent)[first:shared // self.page_tokens]
+
+    def drop_leading(self, key, pages: int) -> int:
+        """Drop a key's first pages, borrowed ones first; returns pages freed."""
+        borrowed = self.borrowed[key]
+        from_borrowed = min(pages, len(borrowed))
+        from_owned = pages - from_borrowed
+        dropped = borrowed[:from_borrowed] + self.owned[key][:from_owned]
+        self.borrowed[key] = borrowed[from_borrowed:]
+        self.owned[key] = self.owned[key][from_owned:]
+        return self.release_pages(dropped)
+
+    def table_pages(self, key) -> list:
+        """Pages a key's block table reads: borrowed first, then its own."""
+        return self.borrowed[key] + self.owned[key]
+
+    def borrowed_tokens(self, key) -> int:
+        return len(self.borrowed[key]) * self.page_tokens
+
+    def release_pages(self, pages) -> int:
+        """Drop one hold on each page in order; returns how many went free."""
+        freed = 0
+        for page in pages:
+            self.holds[page] -= 1
+            if self.holds[page] == 0:
+                self.free.append(page)
+                freed += 1
+        return freed
+
+    def free_key(self, key) -> int:
+        pages = self.owned.pop(key)
+        borrowed = self.borrowed.pop(key)
+        self.tokens.pop(key)
+        self.pinned.discard(key)
+        self._forget_retained(key)
+        return self.release_pages(borrowed + pages)
+
+    def pin(self, key) -> None:
+        if key not in self.owned:
+            raise KeyError(key)
+        self._forget_retained(key)
+        self.pinned.add(key)
+
+    def _forget_retained(self, key):
+        self._retained_pages -= self._retained_sizes.pop(key, 0)
+        self.retained.pop(key, None)
+        self._retained_versions.pop(key, None)
+
+    def retain(self, key, priority=None) -> None:
+        """Make a resident key evictable after its current use (arena.py:153-179)."""
+        if key not in self.owned:
+            raise KeyError(key)
+        self.pinned.discard(key)
+        prefix_tokens = self.tokens[key]
+        self._forget_retained(key)
+        # pages eviction would free now: the ones this key alone holds
+        pages = sum(1 for page in self.table_pages(key) if self.holds[page] == 1)
+        self.retained[key] = prefix_tokens
+        self._retained_sizes[key] = pages
+        self._retained_pages += pages
+        self._retention_version += 1
+        version = self._retention_version
+        self._retained_versions[key] = version
+        if priority is None:
+            if self.retention_policy is not None:
+                priority = self.retention_policy.priority(
+                    key, prefix_tokens, max(1, pages))
+            else:
+                priority = (prefix_tokens / max(1, pages),)
+        heapq.heappush(self._retained_heap,
+                       (priority, version, key, pages, prefix_tokens))
+
+    def configure_retention(self, policy, cap_pages: int) -> None:
+        if not 0 <= cap_pages <= self.n_pages:
+            raise ValueError("retention capacity must fit inside the arena")
+        self.retention_policy = policy
+        self.retention_cap_pages = cap_pages
+        keys = list(self.retained)
+        self._retained_heap.clear()
+        for key in keys:
+            self.retain(key)
+
+    def pop_retained_victim(self, keep=frozenset()):
+        """Remove the retained key with the lowest priority, skipping `keep`."""
+        passed = []
+        victim = None
+        while self._retained_heap:
+            entry = heapq.heappop(self._retained_heap)
+            _, version, key, pages, prefix_tokens = entry
+            if self._retained_versions.get(key) != version:
+                continue  # stale entry
+            if key in keep:
+                passed.append(entry)
+                continue
+            self._forget_retained(key)
+            victim = (key, pages, prefix_tokens)
+            break
+        for entry in passed:
+            heapq.heappush(self._retained_heap, entry)
+        return victim
+
+    def rewind(self, key, tokens: int) -> int:
+        """Keep the first `tokens` and free the trailing own pages."""
+        if key not in self.owned:
+            raise KeyError(key)
+        borrowed = self.borrowed_tokens(key)
+        capacity = borrowed + len(self.owned[key]) * self.page_tokens
+        if tokens < borrowed or tokens > capacity:
+            raise ValueError("rewind tokens leave the resident capacity")
+        keep = self.pages_needed(tokens) - len(self.borrowed[key])
+        released = self.owned[key][keep:]
+        self.owned[key] = self.owned[key][:keep]
+        self.tokens[key] = tokens
+        freed = self.release_pages(released)
+        if key in self.retained:
+            self.retain(key)
+        return freed
+
+    def grow(self, key, capacity_tokens: int):
+        """Own pages up to capacity_tokens; None when the free stack is short."""
+        if key not in self.owned:
+            raise KeyError(key)
+        need = (self.pages_needed(capacity_tokens) - len(self.borrowed[key])
+                - len(self.owned[key]))
+        if need <= 0:
+            return 0
+        if need > len(self.free):
+            return None
+        added = [self.free.pop() for _ in range(need)]
+        self.owned[key].extend(added)
+        for page in added:
+            self.holds[page] += 1
+        return need
+
+    def row_indices(self, key, tokens=None):
+        """Arena rows of the key's first `tokens` tokens (all by default)."""
+        left = self.tokens[key] if tokens is None else tokens
+        rows = []
+        for page in self.table_pages(key):
+            take = min(left, self.page_tokens)
+            base = page * self.page_tokens
+            rows.extend(range(base, base + take))
+            left -= take
+        return rows
+
+    @property
+    def free_pages(self) -> int:
+        return len(self.free)
+
+    @property
+    def resident_tokens(self) -> int:
+        return sum(self.tokens.values())
+
+    @property
+    def retained_pages(self) -> int:
+        return self._retained_pages
+
+    @property
+    def retained_prefix_tokens(self) -> int:
+        return sum(self.tokens[key] for key in self.retained)
+
+
+def _evict_event(key, prefix_tokens):
+    """Answer-sink entry for an evicted (alias, document) key (arena.py:279-294)."""
+    if not (isinstance(key, tuple) and len(key) == 2):
+        return None
+    alias, document = key
+    if not isinstance(alias, str):
+        return None
+    try:
+        document = int(document)
+    except (TypeError, ValueError):
+        return None
+    return {"kind": "evict", "alias": alias, "document": document,
+            "tokens": int(prefix_tokens)}
+
+
+class KVArena:
+    """Device K/V pools per layer plus the page accounting.
+
+    The method surface is the reference's (arena.py:8-24) minus the sliding
+    window, which only DiffusionGemma uses. `allocate=False` builds the
+    accounting and row maps only (host-side tests and planning).
+    """
+
+    def __init__(self, n_layers: int, n_pages: int, page_tokens: int,
+                 n_kv: int, d_head: int, dtype=None, device="cuda",
+                 layer_kv=None, sliding_layers=(), sliding_window=0,
+                 n_sliding_pages=0, allocate=True):
+        import torch
+        self.torch = torch
+        if sliding_window or n_sliding_pages or tuple(sliding_layers):
+            raise ValueError("sliding-window pools are not part of this build")
+        self.dtype = dtype or torch.bfloat16
+        self.device = device
+        self.pinned = str(device).startswith("cuda")
+        shapes = ([(n_kv, d_head)] * n_layers if layer_kv is None
+                  else [tuple(s) for s in layer_kv])
+        if len(shapes) != n_layers:
+            raise ValueError(f"layer_kv names {len(shapes)} layers, the arena "
+                             f"has {n_layers}")
+        self.shapes = shapes
+        self.sliding_layers = frozenset()
+        self.window = 0
+        self.sliding = None
+        self._allocate = allocate
+        self._build(n_pages, page_tokens)
+        self.reset_stats()
+
+    def _build(self, n_pages, page_tokens):
+        torch = self.torch
+        self.accounting = PageArena(n_pages, page_tokens)
+        self.k, self.v = [], []
+        if self._allocate:
+            for heads, dim in self.shapes:
+                self.k.append(torch.empty(layout.k_pool_shape(n_pages, heads, dim, page_tokens),
+                                          dtype=self.dtype, device=self.device))
+                self.v.append(torch.empty(layout.v_pool_shape(n_pages, heads, dim, page_tokens),
+                                          dtype=self.dtype, device=self.device))
+        self._capacity_rows = {}   # key -> np.int64 rows of every claimed page
+        self._holds = {}           # key -> queued borrowers
+        self._deferred = set()     # held keys already freed by their operator
+
+    def resize(self, n_pages: int, n_sliding_pages: int = 0, *,
+               free_resident: bool = False) -> None:
+        if n_sliding_pages:
+            raise ValueError("sliding-window pools are not part of this build")
+        if free_resident:
+            self.drop_holds()
+            for key in self.resident_keys():
+                self.free_key(key)
+        if self.accounting.owned:
+            raise RuntimeError("the arena holds keys; free them before resizing")
+        if n_pages == self.n_pages:
+            return
+        page_tokens = self.page_tokens
+        self.k = self.v = None
+        self._build(n_pages, page_tokens)
+
+    def reset_stats(self):
+        self.evicted_keys = 0
+        self.evicted_pages = 0
+        self.evicted_prefix_tokens = 0
+
+    # ---- window API (no sliding layers in this build) -----------------
+
+    @property
+    def has_sliding(self) -> bool:
+        return False
+
+    def origin(self, base_tokens: int) -> int:
+        return 0
+
+    def sliding_start(self, key) -> int:
+        return 0
+
+    def keep_window(self, key, shared: int) -> None:
+        return None
+
+    def trim_window(self, key) -> int:
+        return 0
+
+    # ---- allocation ---------------------------------------------------
+
+    def alloc(self, key, tokens: int, capacity_tokens=None, base_tokens=None,
+              sliding_tokens=None, borrow=None):
+        capacity = tokens if capacity_tokens is None else capacity_tokens
+        borrowed = self._borrow_plan(borrow)
+        pages = self.accounting.alloc(key, tokens, capacity, borrowed=borrowed)
+        if pages is None:
+            return None
+        self._refresh_rows(key)
+        return pages
+
+    def can_borrow(self, parent, shared: int) -> bool:
+        return (parent in self.accounting.owned
+                and shared <= self.accounting.tokens[parent])
+
+    def _borrow_plan(self, borrow):
+        if borrow is None:
+            return []
+        parent, shared = borrow
+        return self.accounting.shared_pages(parent, shared)
+
+    def _refresh_rows(self, key):
+        """Rows of every page in the key's table, page * page_tokens + slot."""
+        pages = np.asarray(self.accounting.table_pages(key), dtype=np.int64)
+        cap = self._capacity_rows.get(key)
+        if cap is None or cap.size != pages.size * self.page_tokens:
+            rows = pages[:, None] * self.page_tokens + np.arange(self.page_tokens,
+                                                                 dtype=np.int64)
+            self._capacity_rows[key] = rows.reshape(-1)
+
+    def pin(self, key):
+        self.accounting.pin(key)
+
+    def retain(self, key, tokens: int, priority=None):
+        """Rewind a prefix and keep it evictable for a later operator."""
+        if not (isinstance(key, tuple) and len(key) == 2):
+            raise TypeError(f"retained keys are (alias, document) pairs, got {key!r}")
+        self.accounting.rewind(key, tokens)
+        self._refresh_rows(key)
+        self.accounting.retain(key, priority)
+        cap = self.accounting.retention_cap_pages
+        before = self.free_pages
+        if cap is not None:
+            self.evict_retained(max(0, self.accounting.retained_pages - cap))
+        return self.free_pages - before
+
+    def evict_retained(self, pages_needed: int) -> tuple:
+        start = self.free_pages
+        return self._evict_until(lambda: self.free_pages - start >= pages_needed)
+
+    def _evict_until(self, satisfied) -> tuple:
+        keys = []
+        while not satisfied():
+            victim = self.accounting.pop_retained_victim(keep=self._holds)
+            if victim is None:
+                break
+            keys.append(victim[0])
+            self.evict_key(victim[0])
+        return tuple(keys)
+
+    def _evict_for_pages(self, need):
+        self._evict_until(lambda: self.accounting.free_pages >= need)
+
+    def evict_key(self, key):
+        prefix_tokens = self.accounting.tokens[key]
+        pages = self.free_key(key)
+        self.evicted_keys += 1
+        self.evicted_pages += pages
+        self.evicted_prefix_tokens += prefix_tokens
+        sink = answer_sink()
+        if sink is not None:
+            event = _evict_event(key, prefix_tokens)
+            if event is not None:
+                sink(event)
+        return pages
+
+    def activate(self, key, tokens: int, capacity_tokens=None, base_tokens=None,
+                 borrow=None):
+        """Make a prefix active, evicting retained KV when required (arena.py:617-658)."""
+        capacity = tokens if capacity_tokens is None else capacity_tokens
+        acc = self.accounting
+        if key in acc.owned:
+            acc.pin(key)
+            need = max(0, acc.pages_needed(capacity) - len(acc.table_pages(key)))
+            self._evict_for_pages(need)
+            if need > acc.free_pages:
+                return None
+            acc.grow(key, capacity)
+            acc.tokens[key] = tokens
+            self._refresh_rows(key)
+            return acc.owned[key]
+        borrowed = self._borrow_plan(borrow)
+        need = acc.pages_needed(capacity) - len(borrowed)
+        self._evict_for_pages(need)
+        pages = self.alloc(key, tokens, capacity, base_tokens, borrow=borrow)
+        if pages is not None:
+            acc.pin(key)
+        return pages
+
+    def alloc_temporary(self, tokens: int, sliding_tokens=None):
+        key = object()
+        pages = self.alloc(key, tokens, base_tokens=0)
+        return None if pages is None else (key, pages)
+
+    # ---- holds ----------------------------------------------------------
+
+    def hold(self, key, borrowers: int) -> None:
+        if borrowers:
+            self._holds[key] = self._holds.get(key, 0) + borrowers
+
+    def release(self, key) -> None:
+        if key not in self._holds:
+            return
+        self._holds[key] -= 1
+        if not self._holds[key]:
+            del self._holds[key]
+            if key in self._deferred:
+                self._deferred.discard(key)
+                self.free_key(key)
+
+    def drop_holds(self, keys=None) -> bool:
+        keys = (list(self._holds) if keys is None
+                else [k for k in keys if k in self._holds])
+        for key in keys:
+            del self._holds[key]
+            if key in self._deferred:
+                self._deferred.discard(key)
+                self.free_key(key)
+        return bool(keys)
+
+    def free_key(self, key):
+        """Free a key's pages now, or once its last hold is released."""
+        if key in self._holds:
+            self._deferred.add(key)
+            return 0
+        self._capacity_rows.pop(key)
+        return self.accounting.free_key(key)
+
+    # ---- residency --------------------------------------------------------
+
+    @property
+    def page_tokens(self) -> int:
+        return self.accounting.page_tokens
+
+    @property
+    def n_pages(self) -> int:
+        return self.accounting.n_pages
+
+    @property
+    def n_sliding_pages(self) -> int:
+        return 0
+
+    @property
+    def free_pages(self) -> int:
+        return self.accounting.free_pages
+
+    def page_cost(self, tokens: int, base_tokens=None) -> int:
+        return self.accounting.pages_needed(tokens)
+
+    def held_cost(self, key) -> int:
+        return len(self.accounting.owned[key])
+
+    def growth_cost(self, key, capacity_tokens: int) -> int:
+        return max(0, self.accounting.pages_needed(capacity_tokens)
+                   - len(self.accounting.table_pages(key)))
+
+    @property
+    def retained_pages(self) -> int:
+        return self.accounting.retained_pages
+
+    @property
+    def retained_prefix_tokens(self) -> int:
+        return self.accounting.retained_prefix_tokens
+
+    @property
+    def retention_cap_pages(self):
+        return self.accounting.retention_cap_pages
+
+    @retention_cap_pages.setter
+    def retention_cap_pages(self, pages) -> None:
+        self.accounting.retention_cap_pages = pages
+
+    def pages_needed(self, tokens: int) -> int:
+        return self.accounting.pages_needed(tokens)
+
+    def configure_retention(self, policy, cap_pages: int) -> None:
+        self.accounting.configure_retention(policy, cap_pages)
+
+    def is_resident(self, key) -> bool:
+        return key in self.accounting.owned
+
+    def resident_keys(self) -> list:
+        return list(self.accounting.owned)
+
+    def retained_keys(self) -> list:
+        return list(self.accounting.retained)
+
+    def owned_pages(self, key) -> list:
+        return self.accounting.table_pages(key)
+
+    def capacity_rows_np(self, key):
+        """int64 numpy rows of every page in the key's table (host)."""
+        return self._capacity_rows[key]
+
+    def capacity_rows(self, key):
+        """Row index tensor (CPU) over every row in the key's pages."""
+        return self.torch.from_numpy(self._capacity_rows[key])
+
+    # ---- tensors for the kernels -----------------------------------------
+
+    def layer_kv(self, layer: int):
+        """K and V pools of one layer in the MI355X page layout."""
+        return self.k[layer], self.v[layer]
+
+    def paged_kv(self, layer: int):
+        return self.k[layer], self.v[layer]
+
+    def block_table(self, keys, pad_to=None):
+        """Block table and token counts of the keys (arena.py:861-872)."""
+        table = self.block_table_rows([self.accounting.table_pages(k) for k in keys],
+                                      pad_to=pad_to)
+        used = self.torch.tensor([self.accounting.tokens[k] for k in keys],
+                                 dtype=self.torch.int32)
+        return table, used
+
+    @staticmethod
+    def block_table_np(pages, pad_to=None):
+        """int32 [len(pages), width] table, zero-padded (arena.py:874-887)."""
+        width = max(len(p) for p in pages)
+        if pad_to:
+            width = max(width, pad_to)
+        table = np.zeros((len(pages), width), dtype=np.int32)
+        for row, p in enumerate(pages):
+            table[row, :len(p)] = p
+        return table
+
+    def block_table_rows(self, pages, pad_to=None):
+        return self.torch.from_numpy(self.block_table_np(pages, pad_to))

@@ -1,0 +1,407 @@
+// Varlen paged attention on bf16 MFMA (gfx950 v_mfma_f32_32x32x16_bf16).
+//
+// One workgroup = one q-tile of 32 query rows of one sequence x 4 query heads
+// that share one KV head (GQA packs the 4 heads into the 4 waves, so each K/V
+// tile is fetched from HBM once for all of them). Per 64-key tile:
+//   S^T = K Q^T   (M = keys, N = queries, K = head dim): each lane ends up
+//                 holding 16 keys of ONE query, so the row max / row sum of the
+//                 online softmax are in-lane plus one cross-half shuffle.
+//   O^T += V^T P^T (M = head dim, N = queries, K = keys): P^T comes straight
+//                 from the S^T registers (a fixed key permutation inside each
+//                 16-key step, mirrored when V^T fragments are read).
+// K tiles are staged in LDS as [key][d]; V tiles as V^T [d][key]. The arena
+// stores V pages already transposed, so the paged gather is a straight copy of
+// 4 KiB page blocks with 16-byte loads; contiguous (chunk-row) V is transposed
+// on its way into LDS.
+#include "common.h"
+
+namespace qh {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+namespace attn {
+constexpr int BQ = 32;          // query rows per tile
+constexpr int BKV = 64;         // keys per KV tile
+constexpr int D = 128;          // head dim
+constexpr int HPW = 4;          // query heads per workgroup (one per wave)
+constexpr int K_LD = D + 8;     // LDS row stride of K (elements): 272 B
+constexpr int VT_LD = BKV + 4;  // LDS row stride of V^T (elements): 136 B
+constexpr int PAGE = 16;
+}  // namespace attn
+
+struct AttnParams {
+  const uint16_t* q;
+  long ldq;
+  int q_rows_total;
+  const int64_t* q_rows;
+  const uint16_t* k_pool;
+  const uint16_t* v_pool;
+  int pool_pages;
+  const int32_t* table;
+  int table_width;
+  const uint16_t* k_rows;
+  const uint16_t* v_rows;
+  int kv_rows_total;
+  const int32_t* cu_k;
+  const int32_t* cu_q;
+  const int32_t* kv_len;
+  int n_seqs;
+  int n_q;
+  int n_kv;
+  float scale_log2;  // softmax_scale * log2(e)
+  uint16_t* out;
+  long ldo;
+  float* lse;
+  long lse_stride;
+  const int32_t* tile_off;  // [n_seqs + 1] exclusive scan of q-tiles
+};
+
+// Exclusive scan of per-sequence q-tile counts into tile_off[0..n_seqs].
+__global__ __launch_bounds__(1024) void attn_tile_scan_kernel(
+    const int32_t* __restrict__ cu_q, int n_seqs, int32_t* __restrict__ tile_off) {
+  __shared__ int32_t warp_sums[16];
+  __shared__ int32_t carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  for (int base = 0; base < n_seqs; base += 1024) {
+    const int s = base + threadIdx.x;
+    int v = 0;
+    if (s < n_seqs) {
+      const int c = cu_q[s + 1] - cu_q[s];
+      v = c > 0 ? (c + attn::BQ - 1) / attn::BQ : 0;
+    }
+    // inclusive scan within the wave
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) warp_sums[wid] = x;
+    __syncthreads();
+    int wave_off = 0;
+    for (int w = 0; w < wid; ++w) wave_off += warp_sums[w];
+    const int c0 = carry;
+    if (s < n_seqs) tile_off[s] = c0 + wave_off + x - v;
+    __syncthreads();
+    if (threadIdx.x == 1023) carry = c0 + wave_off + x;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) tile_off[n_seqs] = carry;
+}
+
+template <bool PAGED, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
+  using namespace attn;
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[BKV * K_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[D * VT_LD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int half = lane >> 5;   // which 4-row half of each 8-row MFMA group
+  const int col = lane & 31;    // query column of the S^T / O^T tiles
+
+  // ---- which sequence and q-tile -------------------------------------------
+  const int b = blockIdx.x;
+  const int total_tiles = p.tile_off[p.n_seqs];
+  if (b >= total_tiles) return;
+  int lo = 0, hi = p.n_seqs - 1;
+  while (lo < hi) {  // largest s with tile_off[s] <= b
+    const int mid = (lo + hi + 1) >> 1;
+    if (p.tile_off[mid] <= b) lo = mid; else hi = mid - 1;
+  }
+  const int s = lo;
+  const int q0 = p.cu_q[s];
+  const int count = p.cu_q[s + 1] - q0;
+  const int n_tiles = (count + BQ - 1) / BQ;
+  const int tq = n_tiles - 1 - (b - p.tile_off[s]);  // heaviest tile first
+  const int i0 = tq * BQ;
+  const int kv_len = p.kv_len[s];
+
+  const int group = p.n_q / p.n_kv;
+  const int hq = blockIdx.y * HPW + wave;
+  const int hk = (blockIdx.y * HPW) / group;
+
+  // keys this tile reads: causal rows i attend keys < kv_len - count + i + 1
+  int kv_end = kv_len;
+  if (CAUSAL) {
+    const int last = min(i0 + BQ, count) - 1;
+    kv_end = min(kv_len, kv_len - count + last + 1);
+  }
+  if (kv_end < 0) kv_end = 0;
+
+  // ---- Q fragments (B operand of S^T = K Q^T) --------------------------------
+  // lane holds Q[query col][16*st + 8*half .. +7] for st = 0..7
+  bf16x8_t qf[8];
+  {
+    const int i = i0 + col;
+    const bool valid = i < count;
+    long row = q0 + i;
+    if (valid && p.q_rows) row = p.q_rows[row];
+    const bool ok = valid && row >= 0 && row < p.q_rows_total;
+    const uint16_t* qp = p.q + row * p.ldq + (long)hq * D + 8 * half;
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      bf16x8 v;
+      if (ok) v = load8(qp + 16 * st);
+      else v.w[0] = v.w[1] = v.w[2] = v.w[3] = 0;
+      qf[st] = *reinterpret_cast<bf16x8_t*>(&v);
+    }
+  }
+
+  f32x16 acc_o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int a = 0; a < 16; ++a) acc_o[db][a] = 0.f;
+  float m_run = -INFINITY;  // running max (log2 domain), same in both halves
+  float l_run = 0.f;        // running sum of this lane's keys
+
+  // query row limit for the mask (exclusive): keys < lim are visible
+  const int my_i = i0 + col;
+  const int lim = CAUSAL ? min(kv_len, kv_len - count + my_i + 1) : kv_len;
+
+  const int n_kv_tiles = (kv_end + BKV - 1) / BKV;
+
+  // ---- staging: 4 x 16 B of K and 4 x 16 B of V per thread per tile ---------
+  bf16x8 kreg[4], vreg[4];
+  auto load_tile = [&](int kt) {
+    const int key0 = kt * BKV;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // K: instruction i covers keys 16i .. 16i+15 (one page when paged)
+      const int key = key0 + 16 * i + (tid >> 4);
+      const int kc = (tid & 15) * 8;
+      bf16x8 kv;
+      kv.w[0] = kv.w[1] = kv.w[2] = kv.w[3] = 0;
+      bf16x8 vv;
+      vv.w[0] = vv.w[1] = vv.w[2] = vv.w[3] = 0;
+      if (PAGED) {
+        const int pidx = (key0 >> 4) + i;  // page index within the sequence
+        const bool page_live = pidx * PAGE < kv_end;
+        int page = page_live ? p.table[(long)s * p.table_width + pidx] : -1;
+        if (page >= p.pool_pages) page = -1;
+        if (page >= 0) {
+          const long blk = ((long)page * p.n_kv + hk) * (PAGE * D);
+          if (key < kv_end) kv = load8(p.k_pool + blk + (tid >> 4) * D + kc);
+          // V^T page block [D][PAGE]: chunk tid covers d = tid/2, slots 8*(tid&1)..
+          vv = load8(p.v_pool + blk + (long)tid * 8);
+          const int slot0 = pidx * PAGE + 8 * (tid & 1);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (slot0 + e >= kv_end) vv.set(e, 0);
+        }
+      } else {
+        if (key < kv_end) {
+          const long row = (long)p.cu_k[s] + key;
+          if (row >= 0 && row < p.kv_rows_total) {
+            kv = load8(p.k_rows + (row * p.n_kv + hk) * D + kc);
+            vv = load8(p.v_rows + (row * p.n_kv + hk) * D + kc);
+          }
+        }
+      }
+      kreg[i] = kv;
+      vreg[i] = vv;
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = 16 * i + (tid >> 4);
+      const int kc = (tid & 15) * 8;
+      store8(k_lds + key * K_LD + kc, kreg[i]);
+      if (PAGED) {
+        const int d = tid >> 1;
+        uint2* dstp = reinterpret_cast<uint2*>(vt_lds + d * VT_LD + 16 * i + 8 * (tid & 1));
+        dstp[0] = make_uint2(vreg[i].w[0], vreg[i].w[1]);
+        dstp[1] = make_uint2(vreg[i].w[2], vreg[i].w[3]);
+      } else {
+        // row-layout V: 8 consecutive d of one key, transposed into V^T
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          vt_lds[(kc + e) * VT_LD + key] =
+              (uint16_t)((vreg[i].w[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+      }
+    }
+  };
+
+  if (n_kv_tiles > 0) load_tile(0);
+  for (int kt = 0; kt < n_kv_tiles; ++kt) {
+    __syncthreads();  // previous tile's LDS reads are done
+    store_tile();
+    if (kt + 1 < n_kv_tiles) load_tile(kt + 1);
+    __syncthreads();
+
+    // ---- S^T = K Q^T over two 32-key blocks -------------------------------
+    f32x16 sacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int a = 0; a < 16; ++a) sacc[kb][a] = 0.f;
+      const uint16_t* kp = k_lds + (32 * kb + col) * K_LD + 8 * half;
+#pragma unroll
+      for (int st = 0; st < 8; ++st) {
+        bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(kp + 16 * st);
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[st], sacc[kb], 0, 0, 0);
+      }
+    }
+    // ---- mask, scale, online softmax --------------------------------------
+    const int key0 = kt * BKV;
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int a = 0; a < 16; ++a) {
+        const int key = key0 + 32 * kb + 8 * (a >> 2) + 4 * half + (a & 3);
+        const float v = key < lim ? sacc[kb][a] * p.scale_log2 : -INFINITY;
+        sacc[kb][a] = v;
+        tmax = fmaxf(tmax, v);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int a = 0; a < 16; ++a) {
+        const float e = (m_new == -INFINITY) ? 0.f : exp2f(sacc[kb][a] - m_new);
+        sacc[kb][a] = e;
+        psum += e;
+      }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int a = 0; a < 16; ++a) acc_o[db][a] *= alpha;
+
+    // ---- O^T += V^T P^T over four 16-key steps ----------------------------
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int kb = t >> 1, b0 = 2 * (t & 1);
+      bf16x8_t pf;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pf[r] = (__bf16)sacc[kb][4 * b0 + r];
+        pf[4 + r] = (__bf16)sacc[kb][4 * (b0 + 1) + r];
+      }
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint16_t* vp = vt_lds + (32 * db + col) * VT_LD + 16 * t + 4 * half;
+        uint2 lo = *reinterpret_cast<const uint2*>(vp);
+        uint2 hi = *reinterpret_cast<const uint2*>(vp + 8);
+        uint32_t w4[4] = {lo.x, lo.y, hi.x, hi.y};
+        bf16x8_t vf = *reinterpret_cast<bf16x8_t*>(w4);
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc_o[db], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- epilogue -----------------------------------------------------------
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (my_i >= count) return;
+  const long qi = q0 + my_i;
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  uint16_t* op = p.out + qi * p.ldo + (long)hq * D;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * db + 8 * g + 4 * half;
+      uint32_t w0 = f32_to_bf16(acc_o[db][4 * g + 0] * inv) |
+                    (f32_to_bf16(acc_o[db][4 * g + 1] * inv) << 16);
+      uint32_t w1 = f32_to_bf16(acc_o[db][4 * g + 2] * inv) |
+                    (f32_to_bf16(acc_o[db][4 * g + 3] * inv) << 16);
+      *reinterpret_cast<uint2*>(op + d) = make_uint2(w0, w1);
+    }
+  if (p.lse && half == 0) {
+    const float lse = l_tot > 0.f ? (m_run + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+    p.lse[(long)hq * p.lse_stride + qi] = lse;
+  }
+}
+
+}  // namespace qh
+
+using namespace qh;
+
+extern "C" size_t qh_attention_workspace_bytes(int n_seqs) {
+  return (size_t)(n_seqs + 1) * sizeof(int32_t) + 256;
+}
+
+extern "C" int qh_attention(const void* q, long ldq, int q_rows_total, const int64_t* q_rows,
+                            const void* k_pool, const void* v_pool, int pool_pages,
+                            const int32_t* table, int table_width, int page_tokens,
+                            const void* k_rows, const void* v_rows, int kv_rows_total,
+                            const int32_t* cu_k, const int32_t* cu_q, const int32_t* kv_len,
+                            int n_seqs, int n_queries, int max_q, int n_q, int n_kv, int d,
+                            float softmax_scale, int causal, void* out, long ldo, float* lse,
+                            long lse_stride, void* workspace, size_t workspace_bytes,
+                            qh_stream_t stream) {
+  QH_REQUIRE(d == attn::D, "attention: head_dim %d unsupported (128 only)", d);
+  QH_REQUIRE(n_q > 0 && n_kv > 0 && n_q % n_kv == 0 && (n_q / n_kv) % attn::HPW == 0,
+             "attention: n_q=%d n_kv=%d needs a GQA group that is a multiple of 4", n_q, n_kv);
+  QH_REQUIRE(n_seqs >= 0 && n_queries >= 0 && max_q >= 0, "attention: negative sizes");
+  if (n_seqs == 0 || n_queries == 0) return QH_OK;
+  QH_REQUIRE(q && cu_q && kv_len && out, "attention: null pointer");
+  QH_REQUIRE(ldq >= (long)n_q * d && ldq % 8 == 0 && ldo >= (long)n_q * d && ldo % 8 == 0,
+             "attention: row strides ldq=%ld ldo=%ld", ldq, ldo);
+  const bool paged = table != nullptr;
+  if (paged) {
+    QH_REQUIRE(k_pool && v_pool && pool_pages > 0 && table_width > 0,
+               "attention: paged call without pools/table");
+    QH_REQUIRE(page_tokens == attn::PAGE, "attention: page_tokens %d unsupported (16 only)",
+               page_tokens);
+  } else {
+    QH_REQUIRE(k_rows && v_rows && cu_k && kv_rows_total > 0,
+               "attention: contiguous call without k_rows/v_rows/cu_k");
+  }
+  QH_REQUIRE(workspace && workspace_bytes >= qh_attention_workspace_bytes(n_seqs),
+             "attention: workspace of %zu bytes needed", qh_attention_workspace_bytes(n_seqs));
+  QH_REQUIRE(((uintptr_t)workspace & 15) == 0, "attention: workspace must be 16-byte aligned");
+  int32_t* tile_off = (int32_t*)workspace;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(attn_tile_scan_kernel, dim3(1), dim3(1024), 0, st, cu_q, n_seqs, tile_off);
+  int rc = launch_status("attention tile scan");
+  if (rc) return rc;
+
+  AttnParams p;
+  p.q = (const uint16_t*)q;
+  p.ldq = ldq;
+  p.q_rows_total = q_rows_total;
+  p.q_rows = q_rows;
+  p.k_pool = (const uint16_t*)k_pool;
+  p.v_pool = (const uint16_t*)v_pool;
+  p.pool_pages = pool_pages;
+  p.table = table;
+  p.table_width = table_width;
+  p.k_rows = (const uint16_t*)k_rows;
+  p.v_rows = (const uint16_t*)v_rows;
+  p.kv_rows_total = kv_rows_total;
+  p.cu_k = cu_k;
+  p.cu_q = cu_q;
+  p.kv_len = kv_len;
+  p.n_seqs = n_seqs;
+  p.n_q = n_q;
+  p.n_kv = n_kv;
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  p.out = (uint16_t*)out;
+  p.ldo = ldo;
+  p.lse = lse;
+  p.lse_stride = lse_stride;
+  p.tile_off = tile_off;
+  // upper bound on the q-tiles: sum ceil(c/32) <= n_queries/32 + n_seqs
+  const long max_tiles = (long)n_queries / attn::BQ + n_seqs;
+  dim3 grid((unsigned)max_tiles, (unsigned)(n_q / attn::HPW));
+  if (paged) {
+    if (causal) hipLaunchKernelGGL((attn_fwd_kernel<true, true>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((attn_fwd_kernel<true, false>), grid, dim3(256), 0, st, p);
+  } else {
+    if (causal) hipLaunchKernelGGL((attn_fwd_kernel<false, true>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((attn_fwd_kernel<false, false>), grid, dim3(256), 0, st, p);
+  }
+  return launch_status("attention");
+}

@@ -1,0 +1,547 @@
+// Memory-bound fused kernels of the Qwen3 layer loop: norm + quant, QK norm +
+// rotary, SiLU + quant, LSE merge + quant, KV append, gathers, final norm
+// and the answer readout. One wave owns one row (or one 128-wide group) so
+// every group reduction is a 16-lane shuffle, and all HBM traffic moves in
+// 16-byte vectors. Built with -ffp-contract=off: each product and sum rounds
+// on its own, as in the reference's op-by-op fp32 expressions.
+#include "common.h"
+
+namespace qh {
+
+// ---------------------------------------------------------------------------
+// add + RMSNorm + 1x128 group quant (attention.py:325-359 fused path;
+// attention.py:143-175 layer-0 path when residual == nullptr).
+// One wave per row; lane l's vector v covers columns (v*64 + l)*8 .. +8, so
+// lanes 16j..16j+15 of one vector hold one 128-wide group.
+template <int VPL>
+__global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
+    const uint16_t* __restrict__ x, long ldx, uint16_t* __restrict__ residual,
+    long ld_res, const uint16_t* __restrict__ w, float eps, int T, int H,
+    uint8_t* __restrict__ out_q, float* __restrict__ scales, int ue8m0) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int nvec = H >> 9;  // vectors of 8 per lane: H / 512
+  float v[VPL][8];
+  float ss = 0.f;
+  const bool fused = residual != nullptr;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    if (i < nvec) {
+      const long col = ((long)i * 64 + lane) * 8;
+      bf16x8 xv = load8(x + (long)t * ldx + col);
+      if (fused) {
+        bf16x8 rv = load8(residual + (long)t * ld_res + col);
+        bf16x8 sum;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float s = xv.get(e) + rv.get(e);
+          v[i][e] = s;
+          sum.set(e, f32_to_bf16(s));
+          ss += s * s;
+        }
+        store8(residual + (long)t * ld_res + col, sum);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          v[i][e] = xv.get(e);
+          ss += v[i][e] * v[i][e];
+        }
+      }
+    }
+  }
+  ss = group_sum<64>(ss);
+  const float rstd = 1.0f / sqrtf(ss / (float)H + eps);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    if (i < nvec) {
+      const long col = ((long)i * 64 + lane) * 8;
+      bf16x8 wv = load8(w + col);
+      float y[8];
+      float amax = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (fused) {
+          y[e] = v[i][e] * rstd * wv.get(e);
+        } else {
+          // vLLM rms_norm: bf16(bf16(x * rstd) * w)
+          y[e] = round_bf16(round_bf16(v[i][e] * rstd) * wv.get(e));
+        }
+        amax = fmaxf(amax, fabsf(y[e]));
+      }
+      amax = group_max<16>(amax);
+      const float scale = group_scale(amax, ue8m0 != 0);
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lo |= quant_e4m3(y[e], scale) << (8 * e);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hi |= quant_e4m3(y[e + 4], scale) << (8 * e);
+      uint2 packed = make_uint2(lo, hi);
+      *reinterpret_cast<uint2*>(out_q + (long)t * H + col) = packed;
+      if ((lane & 15) == 0) scales[(long)(col >> 7) * T + t] = scale;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 1x128 group quant of bf16 rows (vLLM per_token_group_quant_fp8).
+// One 16-lane group per 128-wide column group.
+__global__ __launch_bounds__(256) void group_quant_kernel(
+    const uint16_t* __restrict__ x, long ldx, int T, int W,
+    uint8_t* __restrict__ out_q, float* __restrict__ scales, int ue8m0) {
+  const int groups = W >> 7;
+  const long gid = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (gid >= (long)T * groups) return;
+  const int t = (int)(gid / groups), g = (int)(gid % groups);
+  const int sub = threadIdx.x & 15;
+  const long col = (long)g * 128 + sub * 8;
+  bf16x8 xv = load8(x + (long)t * ldx + col);
+  float amax = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(xv.get(e)));
+  amax = group_max<16>(amax);
+  const float scale = group_scale(amax, ue8m0 != 0);
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) lo |= quant_e4m3(xv.get(e), scale) << (8 * e);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) hi |= quant_e4m3(xv.get(e + 4), scale) << (8 * e);
+  *reinterpret_cast<uint2*>(out_q + (long)t * W + col) = make_uint2(lo, hi);
+  if (sub == 0) scales[(long)g * T + t] = scale;
+}
+
+// ---------------------------------------------------------------------------
+// SiLU(gate) * up + group quant (attention.py:300-323).
+__global__ __launch_bounds__(256) void silu_mul_quant_kernel(
+    const uint16_t* __restrict__ gu, long ld, int T, int I,
+    uint8_t* __restrict__ out_q, float* __restrict__ scales, int ue8m0) {
+  const int groups = I >> 7;
+  const long gid = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (gid >= (long)T * groups) return;
+  const int t = (int)(gid / groups), g = (int)(gid % groups);
+  const int sub = threadIdx.x & 15;
+  const long col = (long)g * 128 + sub * 8;
+  bf16x8 gv = load8(gu + (long)t * ld + col);
+  bf16x8 uv = load8(gu + (long)t * ld + I + col);
+  float y[8];
+  float amax = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float gate = gv.get(e);
+    const float sig = 1.0f / (1.0f + expf(-gate));
+    y[e] = gate * sig * uv.get(e);
+    amax = fmaxf(amax, fabsf(y[e]));
+  }
+  amax = group_max<16>(amax);
+  const float scale = group_scale(amax, ue8m0 != 0);
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) lo |= quant_e4m3(y[e], scale) << (8 * e);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) hi |= quant_e4m3(y[e + 4], scale) << (8 * e);
+  *reinterpret_cast<uint2*>(out_q + (long)t * I + col) = make_uint2(lo, hi);
+  if (sub == 0) scales[(long)g * T + t] = scale;
+}
+
+// ---------------------------------------------------------------------------
+// Per-head RMSNorm + NeoX rotary for q and k, copy for v (attention.py:361-409).
+// A 16-lane group owns one 128-wide head slot; slot s reads qkv columns
+// s*128.. (q heads, then k heads, then v heads). Lane j < 8 holds the first
+// half's columns 8j..8j+7, lane j >= 8 the matching second-half columns.
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    const uint16_t* __restrict__ qkv, long ld_qkv,
+    const int64_t* __restrict__ positions, const uint16_t* __restrict__ cos_sin,
+    int max_pos, const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
+    float eps, int T, int n_q, int n_kv, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out) {
+  const int t = blockIdx.x;
+  const int slot = blockIdx.y * 16 + (threadIdx.x >> 4);
+  const int j = threadIdx.x & 15;
+  const int total = n_q + 2 * n_kv;
+  if (slot >= total) return;
+  const uint16_t* src = qkv + (long)t * ld_qkv + (long)slot * 128 + j * 8;
+  bf16x8 xv = load8(src);
+  if (slot >= n_q + n_kv) {
+    store8(v_out + ((long)t * n_kv + (slot - n_q - n_kv)) * 128 + j * 8, xv);
+    return;
+  }
+  const bool is_q = slot < n_q;
+  const uint16_t* wt = is_q ? qw : kw;
+  // sum of squares: the first half's and the second half's, then together
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += xv.get(e) * xv.get(e);
+  ss = group_sum<8>(ss);                     // within each half
+  const float other = __shfl_xor(ss, 8, kWave);
+  const float total_ss = (j < 8) ? ss + other : other + ss;
+  const float rstd = 1.0f / sqrtf(total_ss / 128.0f + eps);
+  bf16x8 wv = load8(wt + j * 8);
+  float n[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) n[e] = xv.get(e) * rstd * wv.get(e);
+  // partner half
+  float p[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(n[e], 8, kWave);
+  int64_t pos = positions[t];
+  pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
+  const int hc = (j & 7) * 8;
+  bf16x8 cv = load8(cos_sin + pos * 128 + hc);
+  bf16x8 sv = load8(cos_sin + pos * 128 + 64 + hc);
+  bf16x8 out;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float c = cv.get(e), s = sv.get(e);
+    float r;
+    if (j < 8) {
+      r = n[e] * c - p[e] * s;   // a' = a cos - b sin
+    } else {
+      r = n[e] * c + p[e] * s;   // b' = b cos + a sin
+    }
+    out.set(e, f32_to_bf16(r));
+  }
+  if (is_q) {
+    store8(q_out + ((long)t * n_q + slot) * 128 + j * 8, out);
+  } else {
+    store8(k_out + ((long)t * n_kv + (slot - n_q)) * 128 + j * 8, out);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// KV append into the paged arena. K pages hold [n_kv][page][d]; V pages hold
+// [n_kv][d][page]. One wave per row pair; K moves as 16-byte vectors, V as
+// 2-byte elements into its transposed page column.
+__global__ __launch_bounds__(256) void kv_scatter_kernel(
+    const uint16_t* __restrict__ k_src, const uint16_t* __restrict__ v_src,
+    uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
+    const int64_t* __restrict__ src, const int64_t* __restrict__ dst, int n,
+    int n_kv, int page) {
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= n) return;
+  const int lane = threadIdx.x & 63;
+  const long s = src[i], r = dst[i];
+  const long pg = r / page, slot = r % page;
+  const int row_vecs = n_kv * 16;  // 8-element vectors per row
+  for (int c = lane; c < row_vecs; c += 64) {
+    const int h = c >> 4, off = (c & 15) * 8;
+    bf16x8 kv = load8(k_src + (s * n_kv + h) * 128 + off);
+    store8(k_pool + ((pg * n_kv + h) * page + slot) * 128 + off, kv);
+    bf16x8 vv = load8(v_src + (s * n_kv + h) * 128 + off);
+    uint16_t* vb = v_pool + ((pg * n_kv + h) * 128 + off) * page + slot;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      vb[(long)e * page] = (uint16_t)((vv.w[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+  }
+}
+
+// Arena row -> arena row copy (the kept partial page of a suffix temporary).
+__global__ __launch_bounds__(256) void kv_copy_kernel(
+    uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
+    const int64_t* __restrict__ src, const int64_t* __restrict__ dst, int n,
+    int n_kv, int page) {
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= n) return;
+  const int lane = threadIdx.x & 63;
+  const long rs = src[i], rd = dst[i];
+  const long ps = rs / page, ss = rs % page, pd = rd / page, sd = rd % page;
+  const int row_vecs = n_kv * 16;
+  for (int c = lane; c < row_vecs; c += 64) {
+    const int h = c >> 4, off = (c & 15) * 8;
+    bf16x8 kv = load8(k_pool + ((ps * n_kv + h) * page + ss) * 128 + off);
+    store8(k_pool + ((pd * n_kv + h) * page + sd) * 128 + off, kv);
+    const uint16_t* vs = v_pool + ((ps * n_kv + h) * 128 + off) * page + ss;
+    uint16_t* vd = v_pool + ((pd * n_kv + h) * 128 + off) * page + sd;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vd[(long)e * page] = vs[(long)e * page];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// LSE merge + per-head quant (attention.py:429-473). One 16-lane group per
+// (row, head): each head is exactly one 128-wide quant group.
+__global__ __launch_bounds__(256) void merge_attn_quant_kernel(
+    const uint16_t* __restrict__ a, const float* __restrict__ lse_a,
+    long lse_a_stride, const uint16_t* __restrict__ b,
+    const float* __restrict__ lse_b, long lse_b_stride,
+    const int32_t* __restrict__ source, int T, int n_h,
+    uint8_t* __restrict__ out_q, float* __restrict__ scales, int ue8m0) {
+  const long gid = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (gid >= (long)T * n_h) return;
+  const int t = (int)(gid / n_h), h = (int)(gid % n_h);
+  const int sub = threadIdx.x & 15;
+  const long col = (long)h * 128 + sub * 8;
+  bf16x8 av = load8(a + (long)t * n_h * 128 + col);
+  const int src = source[t];
+  float y[8];
+  if (src >= 0) {
+    bf16x8 bv = load8(b + (long)src * n_h * 128 + col);
+    const float la = lse_a[(long)h * lse_a_stride + t];
+    const float lb = lse_b[(long)h * lse_b_stride + src];
+    const float wgt = round_bf16(1.0f / (1.0f + expf(-(lb - la))));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float av_e = av.get(e);
+      y[e] = round_bf16(av_e + (bv.get(e) - av_e) * wgt);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = av.get(e);
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(y[e]));
+  amax = group_max<16>(amax);
+  const float scale = group_scale(amax, ue8m0 != 0);
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) lo |= quant_e4m3(y[e], scale) << (8 * e);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) hi |= quant_e4m3(y[e + 4], scale) << (8 * e);
+  *reinterpret_cast<uint2*>(out_q + (long)t * n_h * 128 + col) = make_uint2(lo, hi);
+  if (sub == 0) scales[(long)h * T + t] = scale;
+}
+
+// ---------------------------------------------------------------------------
+// Row gather of bf16 rows (embedding lookup, index_select).
+__global__ __launch_bounds__(256) void gather_rows_kernel(
+    const uint16_t* __restrict__ table, long ld_table,
+    const int64_t* __restrict__ idx, int n, int W, uint16_t* __restrict__ out) {
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= n) return;
+  const int lane = threadIdx.x & 63;
+  const long r = idx[i];
+  for (int c = lane * 8; c < W; c += 512)
+    store8(out + (long)i * W + c, load8(table + r * ld_table + c));
+}
+
+// ---------------------------------------------------------------------------
+// vLLM fused_add_rms_norm on gathered rows: z = bf16(h + r);
+// out = bf16(bf16(z * rstd) * w). One wave per answer row.
+__global__ __launch_bounds__(256) void final_norm_kernel(
+    const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ residual,
+    const int64_t* __restrict__ idx, int R, int H, const uint16_t* __restrict__ w,
+    float eps, uint16_t* __restrict__ out) {
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= R) return;
+  const int lane = threadIdx.x & 63;
+  const long r = idx[i];
+  float ss = 0.f;
+  for (int c = lane * 8; c < H; c += 512) {
+    bf16x8 hv = load8(hidden + r * H + c);
+    bf16x8 rv = load8(residual + r * H + c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float z = round_bf16(hv.get(e) + rv.get(e));
+      ss += z * z;
+    }
+  }
+  ss = group_sum<64>(ss);
+  const float rstd = 1.0f / sqrtf(ss / (float)H + eps);
+  for (int c = lane * 8; c < H; c += 512) {
+    bf16x8 hv = load8(hidden + r * H + c);
+    bf16x8 rv = load8(residual + r * H + c);
+    bf16x8 wv = load8(w + c);
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float z = round_bf16(hv.get(e) + rv.get(e));
+      o.set(e, f32_to_bf16(round_bf16(z * rstd) * wv.get(e)));
+    }
+    store8(out + (long)i * H + c, o);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Answer readout: per row, bf16 scores against the retained answer rows,
+// strict TRUE > FALSE compare (readout.py:45-49, :70-79).
+__global__ __launch_bounds__(256) void answer_bits_kernel(
+    const uint16_t* __restrict__ normed, int R, int H,
+    const uint16_t* __restrict__ w_ans, int n_ans,
+    const uint8_t* __restrict__ is_true, uint8_t* __restrict__ bits,
+    float* __restrict__ margin) {
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= R) return;
+  const int lane = threadIdx.x & 63;
+  float best_t = -INFINITY, best_f = -INFINITY;
+  for (int a = 0; a < n_ans; ++a) {
+    float acc = 0.f;
+    for (int c = lane * 8; c < H; c += 512) {
+      bf16x8 nv = load8(normed + (long)i * H + c);
+      bf16x8 wv = load8(w_ans + (long)a * H + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += nv.get(e) * wv.get(e);
+    }
+    acc = group_sum<64>(acc);
+    const float score = round_bf16(acc);
+    if (is_true[a]) best_t = fmaxf(best_t, score);
+    else best_f = fmaxf(best_f, score);
+  }
+  if (lane == 0) {
+    bits[i] = best_t > best_f ? 1 : 0;
+    if (margin) margin[i] = best_t - best_f;
+  }
+}
+
+}  // namespace qh
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+using namespace qh;
+
+static inline unsigned blocks_for(long items, int per_block) {
+  return (unsigned)((items + per_block - 1) / per_block);
+}
+
+extern "C" int qh_add_rmsnorm_quant(const void* x, long ldx, void* residual,
+                                    long ld_res, const void* w, float eps,
+                                    int T, int H, void* out_q, float* scales,
+                                    int ue8m0, qh_stream_t stream) {
+  QH_REQUIRE(x && w && out_q && scales, "add_rmsnorm_quant: null pointer");
+  QH_REQUIRE(T >= 0, "add_rmsnorm_quant: T=%d", T);
+  QH_REQUIRE(H > 0 && H % 512 == 0 && H <= 8192,
+             "add_rmsnorm_quant: H=%d must be a positive multiple of 512 up to 8192", H);
+  QH_REQUIRE(ldx >= H && (!residual || ld_res >= H), "add_rmsnorm_quant: row stride");
+  QH_REQUIRE(ldx % 8 == 0 && (!residual || ld_res % 8 == 0),
+             "add_rmsnorm_quant: row strides must be multiples of 8");
+  if (T == 0) return QH_OK;
+  dim3 grid(blocks_for(T, 4)), block(256);
+  const int vpl = H / 512;
+  auto args = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, block, 0, (hipStream_t)stream,
+                       (const uint16_t*)x, ldx, (uint16_t*)residual, ld_res,
+                       (const uint16_t*)w, eps, T, H, (uint8_t*)out_q, scales, ue8m0);
+  };
+  if (vpl <= 5) args(add_rmsnorm_quant_kernel<5>);
+  else if (vpl <= 10) args(add_rmsnorm_quant_kernel<10>);
+  else args(add_rmsnorm_quant_kernel<16>);
+  return launch_status("add_rmsnorm_quant");
+}
+
+extern "C" int qh_group_quant(const void* x, long ldx, int T, int W, void* out_q,
+                              float* scales, int ue8m0, qh_stream_t stream) {
+  QH_REQUIRE(x && out_q && scales, "group_quant: null pointer");
+  QH_REQUIRE(T >= 0 && W > 0 && W % 128 == 0, "group_quant: W=%d must be a multiple of 128", W);
+  QH_REQUIRE(ldx >= W && ldx % 8 == 0, "group_quant: row stride %ld", ldx);
+  if (T == 0) return QH_OK;
+  const long groups = (long)T * (W / 128);
+  hipLaunchKernelGGL(group_quant_kernel, dim3(blocks_for(groups, 16)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, ldx, T, W,
+                     (uint8_t*)out_q, scales, ue8m0);
+  return launch_status("group_quant");
+}
+
+extern "C" int qh_silu_mul_quant(const void* gate_up, long ld, int T, int I,
+                                 void* out_q, float* scales, int ue8m0,
+                                 qh_stream_t stream) {
+  QH_REQUIRE(gate_up && out_q && scales, "silu_mul_quant: null pointer");
+  QH_REQUIRE(T >= 0 && I > 0 && I % 128 == 0, "silu_mul_quant: I=%d must be a multiple of 128", I);
+  QH_REQUIRE(ld >= 2L * I && ld % 8 == 0, "silu_mul_quant: row stride %ld", ld);
+  if (T == 0) return QH_OK;
+  const long groups = (long)T * (I / 128);
+  hipLaunchKernelGGL(silu_mul_quant_kernel, dim3(blocks_for(groups, 16)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)gate_up, ld, T, I,
+                     (uint8_t*)out_q, scales, ue8m0);
+  return launch_status("silu_mul_quant");
+}
+
+extern "C" int qh_qk_norm_rope(const void* qkv, long ld_qkv, const int64_t* positions,
+                               const void* cos_sin, int max_pos, const void* qw,
+                               const void* kw, float eps, int T, int n_q, int n_kv,
+                               int d, void* q_out, void* k_out, void* v_out,
+                               qh_stream_t stream) {
+  QH_REQUIRE(qkv && positions && cos_sin && qw && kw && q_out && k_out && v_out,
+             "qk_norm_rope: null pointer");
+  QH_REQUIRE(d == 128, "qk_norm_rope: head_dim %d unsupported (128 only)", d);
+  QH_REQUIRE(n_q > 0 && n_kv > 0 && T >= 0 && max_pos > 0, "qk_norm_rope: geometry");
+  QH_REQUIRE(ld_qkv >= (long)(n_q + 2 * n_kv) * d && ld_qkv % 8 == 0,
+             "qk_norm_rope: row stride %ld", ld_qkv);
+  if (T == 0) return QH_OK;
+  dim3 grid(T, blocks_for(n_q + 2 * n_kv, 16));
+  hipLaunchKernelGGL(qk_norm_rope_kernel, grid, dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)qkv, ld_qkv, positions, (const uint16_t*)cos_sin,
+                     max_pos, (const uint16_t*)qw, (const uint16_t*)kw, eps, T, n_q,
+                     n_kv, (uint16_t*)q_out, (uint16_t*)k_out, (uint16_t*)v_out);
+  return launch_status("qk_norm_rope");
+}
+
+extern "C" int qh_kv_row_scatter(const void* k_src, const void* v_src, void* k_pool,
+                                 void* v_pool, const int64_t* src, const int64_t* dst,
+                                 int n, int n_kv, int d, int page_tokens,
+                                 qh_stream_t stream) {
+  QH_REQUIRE(d == 128, "kv_row_scatter: head_dim %d unsupported", d);
+  QH_REQUIRE(n >= 0 && n_kv > 0 && page_tokens > 0, "kv_row_scatter: geometry");
+  if (n == 0) return QH_OK;
+  QH_REQUIRE(k_src && v_src && k_pool && v_pool && src && dst, "kv_row_scatter: null pointer");
+  hipLaunchKernelGGL(kv_scatter_kernel, dim3(blocks_for(n, 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)k_src, (const uint16_t*)v_src,
+                     (uint16_t*)k_pool, (uint16_t*)v_pool, src, dst, n, n_kv, page_tokens);
+  return launch_status("kv_row_scatter");
+}
+
+extern "C" int qh_kv_row_copy(void* k_pool, void* v_pool, const int64_t* src,
+                              const int64_t* dst, int n, int n_kv, int d,
+                              int page_tokens, qh_stream_t stream) {
+  QH_REQUIRE(d == 128, "kv_row_copy: head_dim %d unsupported", d);
+  QH_REQUIRE(n >= 0 && n_kv > 0 && page_tokens > 0, "kv_row_copy: geometry");
+  if (n == 0) return QH_OK;
+  QH_REQUIRE(k_pool && v_pool && src && dst, "kv_row_copy: null pointer");
+  hipLaunchKernelGGL(kv_copy_kernel, dim3(blocks_for(n, 4)), dim3(256), 0,
+                     (hipStream_t)stream, (uint16_t*)k_pool, (uint16_t*)v_pool, src, dst,
+                     n, n_kv, page_tokens);
+  return launch_status("kv_row_copy");
+}
+
+extern "C" int qh_merge_attn_quant(const void* out_a, const float* lse_a,
+                                   long lse_a_stride, const void* out_b,
+                                   const float* lse_b, long lse_b_stride,
+                                   const int32_t* source, int T, int n_h, void* out_q,
+                                   float* scales, int ue8m0, qh_stream_t stream) {
+  QH_REQUIRE(out_a && lse_a && source && out_q && scales, "merge_attn_quant: null pointer");
+  QH_REQUIRE(T >= 0 && n_h > 0, "merge_attn_quant: geometry");
+  if (T == 0) return QH_OK;
+  QH_REQUIRE(out_b && lse_b, "merge_attn_quant: out_b/lse_b null");
+  const long groups = (long)T * n_h;
+  hipLaunchKernelGGL(merge_attn_quant_kernel, dim3(blocks_for(groups, 16)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)out_a, lse_a, lse_a_stride,
+                     (const uint16_t*)out_b, lse_b, lse_b_stride, source, T, n_h,
+                     (uint8_t*)out_q, scales, ue8m0);
+  return launch_status("merge_attn_quant");
+}
+
+extern "C" int qh_gather_rows(const void* table, long ld_table, const int64_t* idx,
+                              int n, int W, void* out, qh_stream_t stream) {
+  QH_REQUIRE(n >= 0 && W > 0 && W % 8 == 0 && ld_table >= W && ld_table % 8 == 0,
+             "gather_rows: geometry W=%d ld=%ld", W, ld_table);
+  if (n == 0) return QH_OK;
+  QH_REQUIRE(table && idx && out, "gather_rows: null pointer");
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks_for(n, 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)table, ld_table, idx, n, W,
+                     (uint16_t*)out);
+  return launch_status("gather_rows");
+}
+
+extern "C" int qh_final_norm(const void* hidden, const void* residual,
+                             const int64_t* final_idx, int R, int H, const void* w,
+                             float eps, void* normed_out, qh_stream_t stream) {
+  QH_REQUIRE(R >= 0 && H > 0 && H % 8 == 0, "final_norm: geometry");
+  if (R == 0) return QH_OK;
+  QH_REQUIRE(hidden && residual && final_idx && w && normed_out, "final_norm: null pointer");
+  hipLaunchKernelGGL(final_norm_kernel, dim3(blocks_for(R, 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)hidden,
+                     (const uint16_t*)residual, final_idx, R, H, (const uint16_t*)w, eps,
+                     (uint16_t*)normed_out);
+  return launch_status("final_norm");
+}
+
+extern "C" int qh_answer_bits(const void* normed, int R, int H, const void* w_ans,
+                              int n_ans, const uint8_t* is_true, uint8_t* bits,
+                              float* margin, qh_stream_t stream) {
+  QH_REQUIRE(R >= 0 && H > 0 && H % 8 == 0 && n_ans > 0, "answer_bits: geometry");
+  if (R == 0) return QH_OK;
+  QH_REQUIRE(normed && w_ans && is_true && bits, "answer_bits: null pointer");
+  hipLaunchKernelGGL(answer_bits_kernel, dim3(blocks_for(R, 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)normed, R, H,
+                     (const uint16_t*)w_ans, n_ans, is_true, bits, margin);
+  return launch_status("answer_bits");
+}

@@ -1,0 +1,28 @@
+// Library status: the per-thread last-error message and launch checks.
+#include "common.h"
+
+namespace qh {
+
+static thread_local char g_error[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+int launch_status(const char* what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(err));
+    return QH_E_HIP;
+  }
+  return QH_OK;
+}
+
+}  // namespace qh
+
+extern "C" int qh_version(void) { return 1; }
+
+extern "C" const char* qh_last_error(void) { return qh::g_error; }

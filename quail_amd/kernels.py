@@ -1,0 +1,247 @@
+"""Torch-facing wrappers of the gfx950 kernels (libquail_hip.so).
+
+Each wrapper checks dtypes and layouts, allocates its outputs with torch on
+the input's device (kernels never allocate), and launches on the current
+torch stream. Activation scales come back the way the reference hands them
+to its GEMM: a (T, G) fp32 view of column-major (G, T) storage
+(attention.py:153-156).
+"""
+
+import torch
+
+from quail_amd import _hip
+
+GROUP = 128        # fp8 quant group, one MFMA K block (attention.py:30)
+PAGE_TOKENS = 16   # tokens per arena page (quail/cost/budgets.py:10)
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _check(t, dtype, name, *, dim=None, contiguous_rows=True):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if dim is not None and t.dim() != dim:
+        raise ValueError(f"{name} must have {dim} dims, got {tuple(t.shape)}")
+    if contiguous_rows and t.stride(-1) != 1:
+        raise ValueError(f"{name} rows must be contiguous")
+
+
+def col_major_scales(n_tokens, width, device):
+    """fp32 scales stored (width/128, T), viewed (T, width/128)."""
+    return torch.empty((width // GROUP, n_tokens), dtype=torch.float32,
+                       device=device).t()
+
+
+def add_rmsnorm_quant(x, weight, eps, residual=None, ue8m0=False):
+    """RMS-normed, fp8-quantized rows; adds the residual (in place) first.
+
+    The Triton add_rms_norm_quant (attention.py:325-359) with a residual,
+    the layer-0 rms_norm + quant (attention.py:158-175) without one.
+    """
+    _check(x, torch.bfloat16, "x", dim=2)
+    _check(weight, torch.bfloat16, "weight", dim=1)
+    T, H = x.shape
+    if residual is not None:
+        _check(residual, torch.bfloat16, "residual", dim=2)
+        if residual.shape != x.shape:
+            raise ValueError("residual shape differs from x")
+    q = torch.empty((T, H), dtype=torch.float8_e4m3fn, device=x.device)
+    scales = col_major_scales(T, H, x.device)
+    _hip.call("qh_add_rmsnorm_quant", _ptr(x), x.stride(0), _ptr(residual),
+              residual.stride(0) if residual is not None else 0, _ptr(weight),
+              float(eps), T, H, _ptr(q), _ptr(scales), int(bool(ue8m0)),
+              _stream())
+    return q, scales
+
+
+def group_quant(x, ue8m0=False):
+    """vLLM per_token_group_quant_fp8 with column-major scales (attention.py:143-151)."""
+    _check(x, torch.bfloat16, "x", dim=2)
+    T, W = x.shape
+    q = torch.empty((T, W), dtype=torch.float8_e4m3fn, device=x.device)
+    scales = col_major_scales(T, W, x.device)
+    _hip.call("qh_group_quant", _ptr(x), x.stride(0), T, W, _ptr(q),
+              _ptr(scales), int(bool(ue8m0)), _stream())
+    return q, scales
+
+
+def fp8_gemm_nt(a, a_scales, w, w_scales, out=None):
+    """out = (a * a_scales) (w * w_scales)^T in bf16 (DeepGEMM fp8_gemm_nt semantics).
+
+    a [M, K] e4m3 with (M, K/128) column-major fp32 scales; w [N, K] e4m3
+    with (N/128, K/128) fp32 block scales.
+    """
+    _check(a, torch.float8_e4m3fn, "a", dim=2)
+    _check(w, torch.float8_e4m3fn, "w", dim=2)
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"K mismatch: a {tuple(a.shape)} w {tuple(w.shape)}")
+    if a_scales.dtype != torch.float32 or tuple(a_scales.shape) != (M, K // GROUP) \
+            or (M > 1 and a_scales.stride(0) != 1) or a_scales.stride(1) != M:
+        raise ValueError("a_scales must be a (M, K/128) view of column-major fp32")
+    if w_scales.dtype != torch.float32 or tuple(w_scales.shape) != (N // GROUP, K // GROUP) \
+            or not w_scales.is_contiguous():
+        raise ValueError("w_scales must be contiguous fp32 (N/128, K/128)")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    _hip.call("qh_fp8_gemm_nt", _ptr(a), a.stride(0), _ptr(a_scales), _ptr(w),
+              w.stride(0), _ptr(w_scales), _ptr(out), out.stride(0), M, N, K,
+              _stream())
+    return out
+
+
+def qk_norm_rope(qkv, positions, cos_sin, q_weight, k_weight, eps, n_q, n_kv,
+                 head_dim):
+    """Per-head RMSNorm + NeoX rotary of q and k, and contiguous v.
+
+    The Triton qk_norm_rope (attention.py:361-409) plus the v copy of
+    Engine.attention (attention.py:793).
+    """
+    _check(qkv, torch.bfloat16, "qkv", dim=2)
+    _check(cos_sin, torch.bfloat16, "cos_sin", dim=2)
+    if positions.dtype != torch.int64 or not positions.is_contiguous():
+        raise ValueError("positions must be contiguous int64")
+    T = qkv.shape[0]
+    dev = qkv.device
+    q = torch.empty((T, n_q * head_dim), dtype=torch.bfloat16, device=dev)
+    k = torch.empty((T, n_kv * head_dim), dtype=torch.bfloat16, device=dev)
+    v = torch.empty((T, n_kv * head_dim), dtype=torch.bfloat16, device=dev)
+    _hip.call("qh_qk_norm_rope", _ptr(qkv), qkv.stride(0), _ptr(positions),
+              _ptr(cos_sin), cos_sin.shape[0], _ptr(q_weight), _ptr(k_weight),
+              float(eps), T, n_q, n_kv, head_dim, _ptr(q), _ptr(k), _ptr(v),
+              _stream())
+    return q, k, v
+
+
+def kv_row_scatter(k_rows, v_rows, k_pool, v_pool, src, dst,
+                   page_tokens=PAGE_TOKENS):
+    """Arena rows dst[i] <- chunk rows src[i] (attention.py:411-427)."""
+    n = src.numel()
+    if n == 0:
+        return
+    if src.dtype != torch.int64 or dst.dtype != torch.int64 or dst.numel() != n:
+        raise ValueError("src/dst must be int64 of equal length")
+    n_kv, d = k_pool.shape[1], k_pool.shape[-1]
+    _hip.call("qh_kv_row_scatter", _ptr(k_rows), _ptr(v_rows), _ptr(k_pool),
+              _ptr(v_pool), _ptr(src), _ptr(dst), n, n_kv, d, page_tokens,
+              _stream())
+
+
+def kv_row_copy(k_pool, v_pool, src, dst, page_tokens=PAGE_TOKENS):
+    """Arena rows dst[i] <- arena rows src[i] (the unified path's tail copy)."""
+    n = src.numel()
+    if n == 0:
+        return
+    n_kv, d = k_pool.shape[1], k_pool.shape[-1]
+    _hip.call("qh_kv_row_copy", _ptr(k_pool), _ptr(v_pool), _ptr(src),
+              _ptr(dst), n, n_kv, d, page_tokens, _stream())
+
+
+def attention(q3, cu_q, kv_len, *, n_queries, max_q, softmax_scale, causal,
+              k_pool=None, v_pool=None, table=None, k_rows=None, v_rows=None,
+              cu_k=None, q_rows=None, n_kv, want_lse=False, out=None):
+    """Varlen attention over paged arena KV (table) or chunk rows (cu_k).
+
+    q3 [rows, n_q, d] bf16. Returns (out [n_queries, n_q, d] bf16, lse
+    [n_q, n_queries] fp32 or None). The three FlashAttention calls of
+    attention.py:850-864 and :939-943.
+    """
+    _check(q3, torch.bfloat16, "q", dim=3)
+    rows, n_q, d = q3.shape
+    n_seqs = cu_q.numel() - 1
+    dev = q3.device
+    if out is None:
+        out = torch.empty((n_queries, n_q, d), dtype=torch.bfloat16, device=dev)
+    lse = (torch.empty((n_q, n_queries), dtype=torch.float32, device=dev)
+           if want_lse else None)
+    ws = torch.empty(_hip.workspace_bytes(n_seqs), dtype=torch.uint8, device=dev)
+    if table is not None:
+        pool_pages = k_pool.shape[0]
+        table_width = table.shape[1]
+        args_kv = (_ptr(k_pool), _ptr(v_pool), pool_pages, _ptr(table),
+                   table_width, PAGE_TOKENS, None, None, 0, None)
+    else:
+        args_kv = (None, None, 0, None, 0, PAGE_TOKENS, _ptr(k_rows),
+                   _ptr(v_rows), k_rows.shape[0], _ptr(cu_k))
+    _hip.call("qh_attention", _ptr(q3), q3.stride(0), rows, _ptr(q_rows),
+              *args_kv, _ptr(cu_q), _ptr(kv_len), n_seqs, int(n_queries),
+              int(max_q), n_q, n_kv, d, float(softmax_scale), int(bool(causal)),
+              _ptr(out), out.stride(0), _ptr(lse),
+              lse.stride(0) if lse is not None else 0, _ptr(ws), ws.numel(),
+              _stream())
+    return out, lse
+
+
+def merge_attn_quant(out_a, lse_a, out_b, lse_b, source, ue8m0=False):
+    """LSE merge of the tree path + per-head fp8 quant (attention.py:429-473).
+
+    lse_a/lse_b are [heads, rows] fp32 (FlashAttention's layout).
+    """
+    T, n_h, d = out_a.shape
+    if d != GROUP:
+        raise ValueError("one quant group per head needs head_dim 128")
+    q = torch.empty((T, n_h * d), dtype=torch.float8_e4m3fn, device=out_a.device)
+    scales = col_major_scales(T, n_h * d, out_a.device)
+    _hip.call("qh_merge_attn_quant", _ptr(out_a), _ptr(lse_a), lse_a.stride(0),
+              _ptr(out_b), _ptr(lse_b), lse_b.stride(0), _ptr(source), T, n_h,
+              _ptr(q), _ptr(scales), int(bool(ue8m0)), _stream())
+    return q, scales
+
+
+def silu_mul_quant(gate_up, ue8m0=False):
+    """silu(gate) * up, fp8-quantized per 1x128 group (attention.py:300-323)."""
+    _check(gate_up, torch.bfloat16, "gate_up", dim=2)
+    T, doubled = gate_up.shape
+    inter = doubled // 2
+    q = torch.empty((T, inter), dtype=torch.float8_e4m3fn, device=gate_up.device)
+    scales = col_major_scales(T, inter, gate_up.device)
+    _hip.call("qh_silu_mul_quant", _ptr(gate_up), gate_up.stride(0), T, inter,
+              _ptr(q), _ptr(scales), int(bool(ue8m0)), _stream())
+    return q, scales
+
+
+def gather_rows(table, idx, out=None):
+    """out[i] = table[idx[i]] for bf16 rows (embedding lookup, index_select)."""
+    _check(table, torch.bfloat16, "table", dim=2)
+    if idx.dtype != torch.int64 or not idx.is_contiguous():
+        raise ValueError("idx must be contiguous int64")
+    n, W = idx.numel(), table.shape[1]
+    if out is None:
+        out = torch.empty((n, W), dtype=torch.bfloat16, device=table.device)
+    _hip.call("qh_gather_rows", _ptr(table), table.stride(0), _ptr(idx), n, W,
+              _ptr(out), _stream())
+    return out
+
+
+def final_norm(hidden, residual, final_idx, weight, eps):
+    """vLLM fused_add_rms_norm on the gathered answer rows (models/qwen3.py:119-124)."""
+    _check(hidden, torch.bfloat16, "hidden", dim=2)
+    _check(residual, torch.bfloat16, "residual", dim=2)
+    if not (hidden.is_contiguous() and residual.is_contiguous()):
+        raise ValueError("hidden and residual must be contiguous")
+    R, H = final_idx.numel(), hidden.shape[1]
+    out = torch.empty((R, H), dtype=torch.bfloat16, device=hidden.device)
+    _hip.call("qh_final_norm", _ptr(hidden), _ptr(residual), _ptr(final_idx), R,
+              H, _ptr(weight), float(eps), _ptr(out), _stream())
+    return out
+
+
+def answer_bits(normed, w_ans, is_true, with_margin=True):
+    """TRUE/FALSE bit per row from the retained answer rows (readout.py:45-49, :70-79)."""
+    _check(normed, torch.bfloat16, "normed", dim=2)
+    R, H = normed.shape
+    bits = torch.empty(R, dtype=torch.uint8, device=normed.device)
+    margin = (torch.empty(R, dtype=torch.float32, device=normed.device)
+              if with_margin else None)
+    _hip.call("qh_answer_bits", _ptr(normed), R, H, _ptr(w_ans), w_ans.shape[0],
+              _ptr(is_true), _ptr(bits), _ptr(margin), _stream())
+    return bits, margin

@@ -1,0 +1,50 @@
+"""Physical KV page layout of the arena, and its logical-row views.
+
+The reference numbers arena rows page * page_tokens + slot and keeps each
+layer's pool as (rows, n_kv, d) (arena.py:343-353, :519-523). This build
+keeps that numbering bit-exactly but stores, per layer,
+
+  K: [n_pages, n_kv, page_tokens, d]   one 4 KiB block per (page, KV head)
+  V: [n_pages, n_kv, d, page_tokens]   the same block transposed
+
+so the attention kernel gathers a page of one KV head as one contiguous
+block and reads V key-contiguous for P.V. The helpers below convert between
+this layout and the reference's (rows, n_kv, d) view; they are used by
+tests and diagnostics, never on the hot path.
+"""
+
+PAGE_TOKENS = 16
+
+
+def k_pool_shape(n_pages, n_kv, head_dim, page_tokens=PAGE_TOKENS):
+    return (n_pages, n_kv, page_tokens, head_dim)
+
+
+def v_pool_shape(n_pages, n_kv, head_dim, page_tokens=PAGE_TOKENS):
+    return (n_pages, n_kv, head_dim, page_tokens)
+
+
+def k_rows(k_pool):
+    """K pool as the reference's (rows, n_kv, d) view (a copy)."""
+    n_pages, n_kv, page, d = k_pool.shape
+    return k_pool.permute(0, 2, 1, 3).reshape(n_pages * page, n_kv, d)
+
+
+def v_rows(v_pool):
+    """V pool as the reference's (rows, n_kv, d) view (a copy)."""
+    n_pages, n_kv, d, page = v_pool.shape
+    return v_pool.permute(0, 3, 1, 2).reshape(n_pages * page, n_kv, d)
+
+
+def k_pool_from_rows(rows, page_tokens=PAGE_TOKENS):
+    """(rows, n_kv, d) -> K pool layout (a copy)."""
+    n_rows, n_kv, d = rows.shape
+    return rows.reshape(n_rows // page_tokens, page_tokens, n_kv, d) \
+        .permute(0, 2, 1, 3).contiguous()
+
+
+def v_pool_from_rows(rows, page_tokens=PAGE_TOKENS):
+    """(rows, n_kv, d) -> V pool layout (a copy)."""
+    n_rows, n_kv, d = rows.shape
+    return rows.reshape(n_rows // page_tokens, page_tokens, n_kv, d) \
+        .permute(0, 2, 3, 1).contiguous()

@@ -1,0 +1,48 @@
+"""The C-ABI library loads on the CPU and exports every declared symbol.
+
+No compute call is made (there is no GPU here); qh_version and the
+workspace-size query are host-only.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from quail_amd import _hip
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "quail_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == sorted(_hip.exported_symbols())
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(_hip.LIB_PATH):
+        pytest.fail(f"{_hip.LIB_PATH} is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(_hip.LIB_PATH)
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} not exported"
+    loaded = _hip.load()
+    assert loaded.qh_version() == 1
+    assert _hip.workspace_bytes(4096) >= 4097 * 4
+
+
+def test_argument_errors_raise_value_error_without_a_gpu():
+    # geometry checks run before any HIP call
+    with pytest.raises(ValueError, match="multiple of 256"):
+        _hip.call("qh_fp8_gemm_nt", None, 128, None, None, 128, None, None, 100,
+                  4, 100, 128, None)
+    with pytest.raises(ValueError, match="head_dim"):
+        _hip.call("qh_attention", None, 0, 0, None, None, None, 0, None, 0, 16,
+                  None, None, 0, None, None, None, 1, 1, 1, 32, 8, 64, 0.1, 1,
+                  None, 0, None, 0, None, 0, None)

@@ -1,0 +1,310 @@
+"""Per-kernel parity of libquail_hip.so against the CPU oracle (MI355X only).
+
+Inputs are seeded and built on the CPU; each kernel runs through the C ABI
+(quail_amd.kernels -> quail_amd._hip) and is compared with oracle.ops on the
+same inputs. Bars: integer/index work bit-exact; fp8 quantization bit-exact
+where the inputs of the rounding are computed identically (group quant),
+otherwise at most 1 e4m3 step on a tiny fraction of elements (sums taken in
+a different order move values across a rounding midpoint); attention
+max-abs <= 2e-3 against fp32.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import ops as ref
+from quail_amd import kernels as K
+from quail_amd import layout
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _e4m3_steps(a, b):
+    """Per-element distance in e4m3 codes (monotone integer mapping)."""
+    def key(q):
+        u = q.view(torch.uint8).to(torch.int32)
+        mag = u & 0x7F
+        return torch.where(u >= 0x80, -mag, mag)
+    return (key(a) - key(b)).abs()
+
+
+def _check_quant(q_gpu, s_gpu, q_ref, s_ref, *, max_frac_off=2e-4, scale_rtol=1e-6):
+    q_gpu, s_gpu = q_gpu.cpu(), s_gpu.cpu()
+    assert torch.allclose(s_gpu, s_ref, rtol=scale_rtol, atol=0), \
+        f"scales differ: max rel {((s_gpu - s_ref).abs() / s_ref).max().item()}"
+    steps = _e4m3_steps(q_gpu, q_ref)
+    assert steps.max().item() <= 1, f"fp8 codes differ by {steps.max().item()} steps"
+    frac = (steps > 0).float().mean().item()
+    assert frac <= max_frac_off, f"{frac:.2e} of fp8 codes differ"
+
+
+@pytest.mark.parametrize("H", [2560, 5120])
+def test_add_rmsnorm_quant_fused_and_plain(H):
+    g = _gen(1)
+    T = 37
+    x = (torch.randn(T, H, generator=g) * 2).to(torch.bfloat16)
+    r = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    eps = 1e-6
+    q_ref, s_ref, r_ref = ref.add_rms_norm_quant(x, r, w, eps)
+    r_gpu = r.to(DEV)
+    q, s = K.add_rmsnorm_quant(x.to(DEV), w.to(DEV), eps, residual=r_gpu)
+    assert torch.equal(r_gpu.cpu(), r_ref), "residual write-back must be bit-exact"
+    _check_quant(q, s, q_ref, s_ref)
+    # layer-0 path: vLLM rms_norm (bf16 out) then group quant
+    q_ref, s_ref = ref.norm_quant_plain(x, w, eps)
+    q, s = K.add_rmsnorm_quant(x.to(DEV), w.to(DEV), eps)
+    _check_quant(q, s, q_ref, s_ref, max_frac_off=2e-3)
+
+
+@pytest.mark.parametrize("ue8m0", [False, True])
+def test_group_quant_bit_exact(ue8m0):
+    g = _gen(2)
+    x = (torch.randn(53, 4096, generator=g) * 3).to(torch.bfloat16)
+    x[3] = 0  # an all-zero row takes the 1e-10 floor
+    q_ref, s_ref = ref.group_quant(x.float(), ue8m0)
+    q, s = K.group_quant(x.to(DEV), ue8m0)
+    assert torch.equal(s.cpu(), s_ref)
+    assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8))
+
+
+def test_e4m3_encoding_matches_torch_at_every_midpoint():
+    # Rows whose amax is 448 quantize with scale exactly 1, so the kernel's
+    # e4m3 encoder sees the raw values: every finite e4m3 value, every
+    # midpoint between neighbours (4 significant bits: exact in bf16) and the
+    # bf16 values either side of each midpoint, both signs. torch's CPU
+    # float8_e4m3fn cast (round to nearest even) is the expected result.
+    codes = torch.arange(0, 0x7F, dtype=torch.uint8)
+    vals = codes.view(torch.float8_e4m3fn).float()
+    mids = ((vals[:-1] + vals[1:]) / 2).to(torch.bfloat16)
+    assert torch.equal(mids.float(), (vals[:-1] + vals[1:]) / 2)
+    bits = mids.view(torch.int16)
+    up = (bits + 1).view(torch.bfloat16)
+    down = (bits - 1).view(torch.bfloat16)
+    pool = torch.cat([vals.to(torch.bfloat16), mids, up, down])
+    pool = torch.cat([pool, -pool])
+    per_row = 127
+    rows = -(-pool.numel() // per_row)
+    flat = torch.zeros(rows * per_row, dtype=torch.bfloat16)
+    flat[:pool.numel()] = pool
+    x = torch.zeros(rows, 128, dtype=torch.bfloat16)
+    x[:, :per_row] = flat.view(rows, per_row)
+    x[:, per_row] = 448.0
+    q_ref, s_ref = ref.group_quant(x.float())
+    assert torch.all(s_ref == 1.0)
+    q, s = K.group_quant(x.to(DEV))
+    assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8))
+
+
+def test_silu_mul_quant():
+    g = _gen(3)
+    T, I = 29, 9728
+    gu = (torch.randn(T, 2 * I, generator=g) * 2).to(torch.bfloat16)
+    q_ref, s_ref = ref.silu_mul_quant(gu)
+    q, s = K.silu_mul_quant(gu.to(DEV))
+    _check_quant(q, s, q_ref, s_ref, max_frac_off=1e-3, scale_rtol=2e-6)
+
+
+def test_qk_norm_rope():
+    g = _gen(4)
+    T, n_q, n_kv, d = 41, 32, 8, 128
+    qkv = torch.randn(T, (n_q + 2 * n_kv) * d, generator=g).to(torch.bfloat16)
+    pos = torch.randint(0, 4000, (T,), generator=g)
+    cs = ref.rope_cache(4096, d, 1e6)
+    qw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    q_ref, k_ref, v_ref = ref.qk_norm_rope(qkv, pos, cs, qw, kw, 1e-6, n_q, n_kv, d)
+    q, k, v = K.qk_norm_rope(qkv.to(DEV), pos.to(DEV), cs.to(DEV), qw.to(DEV),
+                             kw.to(DEV), 1e-6, n_q, n_kv, d)
+    assert torch.equal(v.cpu(), v_ref)
+    for got, want in ((q.cpu(), q_ref), (k.cpu(), k_ref)):
+        diff = (got.float() - want.float()).abs()
+        ulp = want.float().abs().clamp(min=1e-30) * 2 ** -7
+        assert (diff <= ulp).all(), f"max diff {diff.max().item()}"
+        assert (diff > 0).float().mean() < 1e-2
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 256, 128), (300, 512, 2560), (517, 6144, 2560),
+                                    (256, 2560, 9728)])
+def test_fp8_gemm_nt(M, N, Kd):
+    g = _gen(5)
+    w = torch.randn(N, Kd, generator=g) * 0.02
+    wq, ws = ref.quantize_weight_blocks(w)
+    x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    xq, xs = ref.group_quant(x.float())
+    want = ref.fp8_gemm(xq, xs, wq, ws, out_dtype=torch.float64)
+    xs_dev = K.col_major_scales(M, Kd, DEV)
+    xs_dev.copy_(xs)
+    got = K.fp8_gemm_nt(xq.to(DEV), xs_dev, wq.to(DEV), ws.to(DEV)).cpu().double()
+    err = (got - want).abs()
+    tol = want.abs() * 2 ** -8 + 1e-3 * want.abs().max()
+    assert (err <= tol).all(), f"max err {err.max().item()} (scale {want.abs().max().item()})"
+
+
+def _paged_case(seed, n_seqs, prefix, max_suffix, n_q=32, n_kv=8, d=128):
+    """Sequences sharing a `prefix`-token node, own suffixes, permuted pages."""
+    g = _gen(seed)
+    page = 16
+    lens = torch.randint(1, max_suffix + 1, (n_seqs,), generator=g).tolist()
+    prefix_pages = -(-prefix // page)
+    need = prefix_pages + sum(-(-(prefix % page + L) // page) + 1 for L in lens)
+    n_pages = need + 8
+    perm = torch.randperm(n_pages, generator=g).tolist()
+    k_rows = (torch.randn(n_pages * page, n_kv, d, generator=g) / math.sqrt(d)).to(torch.bfloat16)
+    v_rows = (torch.randn(n_pages * page, n_kv, d, generator=g) / math.sqrt(d)).to(torch.bfloat16)
+    shared = perm[:prefix_pages]
+    cursor = prefix_pages
+    tables, used = [], []
+    for L in lens:
+        total = prefix + L
+        pages = list(shared[:prefix // page])
+        while len(pages) * page < total:
+            pages.append(perm[cursor])
+            cursor += 1
+        # a partially shared last prefix page is copied into the sequence's own page
+        tables.append(pages)
+        used.append(total)
+    width = max(map(len, tables))
+    table = torch.zeros(n_seqs, width, dtype=torch.int32)
+    for i, p in enumerate(tables):
+        table[i, :len(p)] = torch.tensor(p, dtype=torch.int32)
+    cu_q = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32)
+    T = int(cu_q[-1])
+    q = (torch.randn(T, n_q, d, generator=g) / math.sqrt(d)).to(torch.bfloat16)
+    return dict(q=q, k_rows=k_rows, v_rows=v_rows, table=table,
+                used=torch.tensor(used, dtype=torch.int32), cu_q=cu_q, lens=lens,
+                n_kv=n_kv, max_q=max(lens))
+
+
+def _run_paged(case, causal, q_rows=None):
+    scale = 1 / math.sqrt(case["q"].shape[-1])
+    kp = layout.k_pool_from_rows(case["k_rows"]).to(DEV)
+    vp = layout.v_pool_from_rows(case["v_rows"]).to(DEV)
+    n_queries = int(case["cu_q"][-1])
+    out, lse = K.attention(case["q"].to(DEV), case["cu_q"].to(DEV), case["used"].to(DEV),
+                           n_queries=n_queries, max_q=case["max_q"], softmax_scale=scale,
+                           causal=causal, k_pool=kp, v_pool=vp, table=case["table"].to(DEV),
+                           q_rows=None if q_rows is None else q_rows.to(DEV),
+                           n_kv=case["n_kv"], want_lse=True)
+    want, want_lse = ref.paged_attention(case["q"], case["k_rows"], case["v_rows"],
+                                         case["cu_q"], case["used"], case["table"],
+                                         scale, causal, q_rows=q_rows)
+    return out.cpu().float(), lse.cpu(), want, want_lse
+
+
+@pytest.mark.parametrize("seed,n_seqs,prefix,max_suffix", [
+    (10, 8, 64, 100), (11, 5, 256, 256), (12, 3, 37, 300), (13, 16, 0, 40)])
+def test_paged_attention_causal(seed, n_seqs, prefix, max_suffix):
+    case = _paged_case(seed, n_seqs, prefix, max_suffix)
+    got, lse, want, want_lse = _run_paged(case, causal=True)
+    err = (got - want).abs().max().item()
+    assert err <= 2e-3, f"max-abs {err}"
+    assert torch.allclose(lse, want_lse, atol=2e-3, rtol=0)
+
+
+def test_paged_attention_noncausal_gathered_rows():
+    case = _paged_case(20, 6, 128, 60)
+    T = int(case["cu_q"][-1])
+    # call B stacks reader rows of a larger packed chunk
+    g = _gen(21)
+    big = torch.randn(T + 50, 32, 128, generator=g).to(torch.bfloat16)
+    rows = torch.randperm(T + 50, generator=g)[:T].sort().values
+    big[rows] = case["q"]
+    case_b = dict(case, q=big)
+    got, lse, want, want_lse = _run_paged(case_b, causal=False, q_rows=rows)
+    assert (got - want).abs().max().item() <= 2e-3
+    assert torch.allclose(lse, want_lse, atol=2e-3, rtol=0)
+
+
+def test_contiguous_causal_attention():
+    g = _gen(30)
+    lens = [1, 17, 64, 65, 200, 3]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0)), dtype=torch.int32)
+    T = int(cu[-1])
+    q = (torch.randn(T, 32, 128, generator=g) / math.sqrt(128)).to(torch.bfloat16)
+    k = (torch.randn(T, 8, 128, generator=g) / math.sqrt(128)).to(torch.bfloat16)
+    v = (torch.randn(T, 8, 128, generator=g) / math.sqrt(128)).to(torch.bfloat16)
+    scale = 1 / math.sqrt(128)
+    kv_len = torch.tensor(lens, dtype=torch.int32)
+    out, lse = K.attention(q.to(DEV), cu.to(DEV), kv_len.to(DEV), n_queries=T,
+                           max_q=max(lens), softmax_scale=scale, causal=True,
+                           k_rows=k.to(DEV), v_rows=v.to(DEV), cu_k=cu.to(DEV),
+                           n_kv=8, want_lse=True)
+    want, want_lse = ref.varlen_attention(q, k, v, cu, scale, causal=True)
+    assert (out.cpu().float() - want).abs().max().item() <= 2e-3
+    assert torch.allclose(lse.cpu(), want_lse, atol=2e-3, rtol=0)
+
+
+def test_merge_attn_quant():
+    g = _gen(40)
+    T, R, H, d = 57, 20, 32, 128
+    a = torch.randn(T, H, d, generator=g).to(torch.bfloat16)
+    b = torch.randn(R, H, d, generator=g).to(torch.bfloat16)
+    la = torch.randn(H, T, generator=g) * 3
+    lb = torch.randn(H, R, generator=g) * 3
+    source = torch.full((T,), -1, dtype=torch.int32)
+    source[torch.randperm(T, generator=g)[:R]] = torch.arange(R, dtype=torch.int32)
+    q_ref, s_ref = ref.merge_attn_quant(a, la, b, lb, source)
+    q, s = K.merge_attn_quant(a.to(DEV), la.to(DEV), b.to(DEV), lb.to(DEV), source.to(DEV))
+    _check_quant(q, s, q_ref, s_ref, max_frac_off=1e-3, scale_rtol=0)
+
+
+def test_kv_row_scatter_and_copy_bit_exact():
+    g = _gen(50)
+    n_pages, n_kv, d = 24, 8, 128
+    rows = n_pages * 16
+    k_pool_rows = torch.randn(rows, n_kv, d, generator=g).to(torch.bfloat16)
+    v_pool_rows = torch.randn(rows, n_kv, d, generator=g).to(torch.bfloat16)
+    T = 70
+    k_src = torch.randn(T, n_kv, d, generator=g).to(torch.bfloat16)
+    v_src = torch.randn(T, n_kv, d, generator=g).to(torch.bfloat16)
+    src = torch.randperm(T, generator=g)[:50]
+    dst = torch.randperm(rows, generator=g)[:50]
+    kp = layout.k_pool_from_rows(k_pool_rows).to(DEV)
+    vp = layout.v_pool_from_rows(v_pool_rows).to(DEV)
+    K.kv_row_scatter(k_src.to(DEV), v_src.to(DEV), kp, vp, src.to(DEV), dst.to(DEV))
+    ref.kv_row_scatter(k_pool_rows, v_pool_rows, k_src, v_src, src, dst)
+    assert torch.equal(layout.k_rows(kp.cpu()), k_pool_rows)
+    assert torch.equal(layout.v_rows(vp.cpu()), v_pool_rows)
+    # pool -> pool copy (tail of a kept page into a temporary)
+    csrc = torch.randperm(rows, generator=g)[:30]
+    cdst = torch.randperm(rows, generator=g)[:30]
+    cdst = cdst[~torch.isin(cdst, csrc)]
+    csrc = csrc[:cdst.numel()]
+    K.kv_row_copy(kp, vp, csrc.to(DEV), cdst.to(DEV))
+    k_pool_rows[cdst] = k_pool_rows[csrc]
+    v_pool_rows[cdst] = v_pool_rows[csrc]
+    assert torch.equal(layout.k_rows(kp.cpu()), k_pool_rows)
+    assert torch.equal(layout.v_rows(vp.cpu()), v_pool_rows)
+
+
+def test_gather_final_norm_and_answer_bits():
+    g = _gen(60)
+    T, H = 90, 2560
+    table = torch.randn(500, H, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, 500, (T,), generator=g)
+    assert torch.equal(K.gather_rows(table.to(DEV), idx.to(DEV)).cpu(), table[idx])
+    hidden = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    resid = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    fin = torch.tensor([3, 17, 89, 0], dtype=torch.int64)
+    want, _ = ref.fused_add_rms_norm(hidden[fin], resid[fin], w, 1e-6)
+    got = K.final_norm(hidden.to(DEV), resid.to(DEV), fin.to(DEV), w.to(DEV), 1e-6).cpu()
+    diff = (got.float() - want.float()).abs()
+    assert (diff <= want.float().abs() * 2 ** -7).all()
+    # readout: 6 retained rows, TRUE = the first three
+    w_ans = (torch.randn(6, H, generator=g) * 0.05).to(torch.bfloat16)
+    is_true = torch.tensor([1, 1, 1, 0, 0, 0], dtype=torch.uint8)
+    normed = torch.randn(64, H, generator=g).to(torch.bfloat16)
+    bits_ref, margin_ref = ref.answer_bits(normed, w_ans, [0, 1, 2], [3, 4, 5])
+    bits, margin = K.answer_bits(normed.to(DEV), w_ans.to(DEV), is_true.to(DEV))
+    clear = margin_ref.abs() > 0.05
+    assert torch.equal(bits.cpu()[clear], bits_ref[clear])
+    assert (margin.cpu() - margin_ref).abs().max().item() < 0.1
