@@ -1,0 +1,145 @@
+"""Qwen3 forward over a packed chunk on the CPU (oracle; tests and cpu_baseline only).
+
+Restates Qwen3Pipeline.forward_chunk of the reference (models/qwen3.py:
+46-77) with the Engine semantics of attention.py (norm_quant :763-769,
+gemm :129-141, qk_norm_rope :361-409, attention_unified :878-953,
+attention_tree :835-870, activation_quant :300-323, final
+fused_add_rms_norm :177-181). KV lives in a logical arena: per layer, K and
+V as (rows, n_kv, d) bf16 indexed by the reference's arena row numbers; the
+chunk's scatter maps write it exactly as the kernels write the device pools.
+"""
+
+import torch
+
+from oracle import ops
+
+
+class OracleArena:
+    """Per-layer logical K/V pools, arena rows page * 16 + slot."""
+
+    def __init__(self, n_layers, n_pages, n_kv, head_dim, page_tokens=16):
+        rows = n_pages * page_tokens
+        self.k = [torch.zeros(rows, n_kv, head_dim, dtype=torch.bfloat16)
+                  for _ in range(n_layers)]
+        self.v = [torch.zeros(rows, n_kv, head_dim, dtype=torch.bfloat16)
+                  for _ in range(n_layers)]
+
+
+def cpu_weights(model):
+    """CPU copies of a quail_amd.model model's tensors, in a flat dict."""
+    inner = model.model
+    w = {"embed": inner.embed_tokens.weight.cpu(), "final_norm": inner.norm.weight.cpu(),
+         "final_eps": inner.norm.variance_epsilon,
+         "cos_sin": model.rotary.cos_sin_cache.cpu(),
+         "answer": model.quail_answer_weights.cpu(),
+         "answer_ids": model.quail_answer_token_ids, "layers": []}
+    for layer in inner.layers:
+        a, m = layer.self_attn, layer.mlp
+        w["layers"].append(dict(
+            qkv=(a.qkv_proj.weight.cpu(), a.qkv_proj.weight_scale.cpu()),
+            o=(a.o_proj.weight.cpu(), a.o_proj.weight_scale.cpu()),
+            gate_up=(m.gate_up_proj.weight.cpu(), m.gate_up_proj.weight_scale.cpu()),
+            down=(m.down_proj.weight.cpu(), m.down_proj.weight_scale.cpu()),
+            q_norm=a.q_norm.weight.cpu(), k_norm=a.k_norm.weight.cpu(),
+            in_norm=layer.input_layernorm.weight.cpu(),
+            post_norm=layer.post_attention_layernorm.weight.cpu(),
+            eps=layer.input_layernorm.variance_epsilon,
+            n_q=a.num_heads, n_kv=a.num_kv_heads, head_dim=a.head_dim))
+    return w
+
+
+class DequantGemm:
+    """fp8 GEMM as dequantize-to-fp32 then one fp32 matmul, weights cached.
+
+    Same sum as ops.fp8_gemm in fp32 accumulation; the CPU baseline uses it
+    (dequantize with block scales, then matmul).
+    """
+
+    def __init__(self):
+        self.cache = {}
+
+    def __call__(self, a_q, a_s, w_q, w_s):
+        key = w_q.data_ptr()
+        w = self.cache.get(key)
+        if w is None:
+            w = ops.dequant_weight(w_q, w_s).T.contiguous()
+            self.cache[key] = w
+        a = ops.dequant_rows(a_q, a_s)
+        return (a @ w).to(torch.bfloat16)
+
+
+def exact_gemm(a_q, a_s, w_q, w_s):
+    return ops.fp8_gemm(a_q, a_s, w_q, w_s)
+
+
+def forward_chunk(w, host, attention_mode, arena, gemm=exact_gemm, ue8m0=False,
+                  page_tokens=16):
+    """The final-normed rows of one chunk, [R, hidden] bf16.
+
+    host: the chunk's staged arrays as numpy (Chunk.host). arena:
+    OracleArena, updated in place by the chunk's KV writes.
+    """
+    t = lambda name: torch.from_numpy(host[name])
+    ids = t("input_ids")
+    pos = t("positions")
+    finals = t("finals")
+    T = ids.numel()
+    hidden = w["embed"][ids]
+    residual = None
+    for li, L in enumerate(w["layers"]):
+        n_q, n_kv, d, eps = L["n_q"], L["n_kv"], L["head_dim"], L["eps"]
+        if residual is None:
+            residual = hidden
+            q_in, q_s = ops.norm_quant_plain(hidden, L["in_norm"], eps, ue8m0)
+        else:
+            q_in, q_s, residual = ops.add_rms_norm_quant(hidden, residual, L["in_norm"],
+                                                         eps, ue8m0)
+        qkv = gemm(q_in, q_s, *L["qkv"])
+        q, k, v = ops.qk_norm_rope(qkv, pos, w["cos_sin"], L["q_norm"], L["k_norm"], eps,
+                                   n_q, n_kv, d)
+        q3, k3, v3 = q.view(T, n_q, d), k.view(T, n_kv, d), v.view(T, n_kv, d)
+        scale = ops.softmax_scale(d)
+        kp, vp = arena.k[li], arena.v[li]
+        if attention_mode == "tree":
+            if "kv_src" in host:
+                ops.kv_row_scatter(kp, vp, k3, v3, t("kv_src"), t("kv_dst"))
+            out_a, lse_a = ops.varlen_attention(q3, k3, v3, t("cu_a"), scale, causal=True)
+            out_a = out_a.to(torch.bfloat16)
+            if "reads_rows" in host:
+                out_b, lse_b = ops.paged_attention(
+                    q3, kp, vp, t("reads_cu_q"), t("reads_used"), t("reads_table"), scale,
+                    causal=False, q_rows=t("reads_rows"), page=page_tokens)
+                o_in, o_s = ops.merge_attn_quant(out_a, lse_a, out_b.to(torch.bfloat16),
+                                                 lse_b, t("reads_source"), ue8m0)
+            else:
+                o_in, o_s = ops.group_quant(out_a.float().view(T, -1), ue8m0)
+        else:
+            if "unified_src" in host:
+                ops.kv_row_scatter(kp, vp, k3, v3, t("unified_src"), t("unified_dst"))
+                if "tail_src" in host:
+                    src, dst = t("tail_src"), t("tail_dst")
+                    kp[dst] = kp[src]
+                    vp[dst] = vp[src]
+                out, _ = ops.paged_attention(q3, kp, vp, t("unified_cu_q"),
+                                             t("unified_used"), t("unified_table"), scale,
+                                             causal=True, page=page_tokens)
+            else:
+                out, _ = ops.varlen_attention(q3, k3, v3, t("cu_a"), scale, causal=True)
+            o_in, o_s = ops.group_quant(out.to(torch.bfloat16).float().view(T, -1), ue8m0)
+        hidden = gemm(o_in, o_s, *L["o"])
+        g_in, g_s, residual = ops.add_rms_norm_quant(hidden, residual, L["post_norm"], eps,
+                                                     ue8m0)
+        gate_up = gemm(g_in, g_s, *L["gate_up"])
+        d_in, d_s = ops.silu_mul_quant(gate_up, ue8m0)
+        hidden = gemm(d_in, d_s, *L["down"])
+    normed, _ = ops.fused_add_rms_norm(hidden[finals], residual[finals], w["final_norm"],
+                                       w["final_eps"])
+    return normed
+
+
+def readout(w, normed, true_ids, false_ids):
+    """(bits, margins) of the final-normed rows (readout.py:45-49, :70-79)."""
+    allowed = list(w["answer_ids"])
+    true_cols = [i for i, t in enumerate(allowed) if t in set(true_ids)]
+    false_cols = [i for i, t in enumerate(allowed) if t in set(false_ids)]
+    return ops.answer_bits(normed, w["answer"], true_cols, false_cols)

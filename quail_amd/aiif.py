@@ -1,0 +1,115 @@
+"""AI.IF filter over rows on one GPU: synthetic workloads and the runner.
+
+The runner wires what the reference's LoadedGpu + execute_single_graph do
+for one filter node (quail/backends/quail/worker.py:46-148; backend.py:
+107-161): build the arena (sized by the budget formulas), the Qwen3
+pipeline and the answer readout, then run loop.run_filter over
+`DocumentPrefixes(instruction, documents)` with the prefix tree deciding
+page borrowing. Rows are synthetic (no dataset or tokenizer offline).
+"""
+
+import time
+
+import numpy as np
+
+from quail_amd import budgets, loop
+from quail_amd.arena import KVArena
+from quail_amd.model import SYNTHETIC_FALSE_IDS, SYNTHETIC_TRUE_IDS
+from quail_amd.qwen3 import Qwen3Pipeline
+from quail_amd.readout import AnswerRows, AsyncAnswers
+from quail_amd.specs import MI355X
+from quail_amd.tokens import prefix_tree
+
+
+def lognormal_lengths(n, median, mean, cap, rng):
+    """Rounded lognormal lengths with the given median and mean, in [1, cap]."""
+    mu = np.log(median)
+    sigma = np.sqrt(2.0 * np.log(mean / median))
+    lens = np.rint(rng.lognormal(mu, sigma, size=n)).astype(np.int64)
+    return np.clip(lens, 1, cap)
+
+
+def synthetic_filter_workload(n_rows, *, prefix_tokens=64, median=180, mean=230,
+                              cap=1024, tail_tokens=24, vocab=151_936, seed=0):
+    """Rows of an AI.IF over a Qwen3-sized vocabulary.
+
+    Every row is a shared `prefix_tokens`-token instruction, then a
+    document of lognormal length (median, mean, capped) of uniform random
+    ids; one question tail of `tail_tokens` ids follows each row.
+    Returns (instruction ids, documents, question tail).
+    """
+    rng = np.random.default_rng(seed)
+    instruction = rng.integers(0, vocab, size=prefix_tokens, dtype=np.int64)
+    lens = lognormal_lengths(n_rows, median, mean, cap, rng)
+    documents = [rng.integers(0, vocab, size=int(L), dtype=np.int64) for L in lens]
+    tail = rng.integers(0, vocab, size=tail_tokens, dtype=np.int64)
+    return instruction, documents, tail
+
+
+class RowPrompts:
+    """Row i = instruction + document i (tokens.DocumentPrefixes), materialised once."""
+
+    def __init__(self, instruction, documents):
+        self.rows = [np.concatenate([instruction, d]) for d in documents]
+
+    def __len__(self):
+        return len(self.rows)
+
+    def __getitem__(self, i):
+        return self.rows[i]
+
+
+class FilterRunner:
+    """One GPU's AI.IF executor: model, arena, pipeline, readout.
+
+    Args:
+        model: a quail_amd.model model (weights on the GPU).
+        spec: its ModelSpec.
+        n_pages: arena pages; None sizes the arena with budgets.arena_pages
+            for `device_spec` (the reference's formula).
+        budget: chunk tokens; None uses budgets.chunk_budget.
+        attention_mode: "unified", "tree" or None (unified).
+        gemm_hook: passed to the engine (GEMM timing in bench.py).
+    """
+
+    def __init__(self, model, spec, *, device_spec=MI355X, n_pages=None, budget=None,
+                 attention_mode=None, ue8m0=False, gemm_hook=None, keep_margins=True,
+                 true_ids=SYNTHETIC_TRUE_IDS, false_ids=SYNTHETIC_FALSE_IDS):
+        import torch
+        self.torch = torch
+        self.spec = spec
+        n_layers = len(model.model.layers)
+        self.budget = budget or budgets.chunk_budget(spec, device_spec)
+        if n_pages is None:
+            n_pages, _ = budgets.arena_pages(spec, device_spec, self.budget)
+        self.arena = KVArena(n_layers, n_pages, budgets.PAGE_TOKENS, spec.n_kv,
+                             spec.d_head, dtype=torch.bfloat16, device="cuda")
+        self.pipeline = Qwen3Pipeline(model, self.arena, spec=spec, ue8m0=ue8m0,
+                                      gemm_hook=gemm_hook)
+        self.rows = AnswerRows(torch, model, true_ids, false_ids)
+        self.answers = AsyncAnswers(torch, self.rows, keep_margins=keep_margins)
+        self.attention_mode = attention_mode
+        self.last = {}
+
+    def run(self, instruction, documents, tail, *, timing=None):
+        """Run the filter; returns (answers per row, stats)."""
+        torch = self.torch
+        docs = RowPrompts(instruction, documents)
+        tree = prefix_tree(docs, budgets.PAGE_TOKENS)
+        self.answers.margins = []
+        stats = {}
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        answers, _, tokens = loop.run_filter(
+            torch, self.arena, self.pipeline, self.answers, docs, [list(tail)],
+            self.budget, timing=timing, arena_writes=True,
+            attention_mode=self.attention_mode, prefix_tree=tree, stats=stats)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        if self.arena.accounting.owned:
+            raise AssertionError("the filter left pages resident")
+        input_tokens = sum(len(d) + len(tail) for d in docs.rows)
+        stats.update(wall_s=wall, fresh_tokens=tokens, input_tokens=input_tokens,
+                     rows=len(docs), shared_tokens=tree.shared_tokens)
+        self.last = stats
+        return [answers[i][0] for i in range(len(docs))], stats

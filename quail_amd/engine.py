@@ -1,0 +1,151 @@
+"""The forward-pass engine: the primitives a model loop calls, on gfx950 kernels.
+
+Same surface as the reference's Engine (quail/backends/quail/executor/
+attention.py:84-953): norm_quant, gemm, qk_norm_rope, attention,
+activation_quant, fused_add_rms_norm. Every primitive launches a kernel of
+libquail_hip.so; nothing falls back to torch math. Two attention paths:
+
+  unified  scatter the chunk's fresh K/V rows into the arena (plus the
+           kept-page tail copies of suffix temporaries), then one paged
+           causal call in which every row reads the KV its document needs
+           (attention.py:878-953); output quantized per 1x128 group.
+  tree     scatter the kept rows; call A: causal over the chunk's own
+           segments (chunk rows); call B: the readers of resident KV read it
+           stacked, non-causal; fused LSE merge + fp8 quant
+           (attention.py:835-870).
+"""
+
+import math
+
+from quail_amd import kernels
+
+GROUP = kernels.GROUP
+
+
+class Engine:
+    """Kernels, quantization and attention over the paged arena.
+
+    Args:
+        arena: KVArena the attention paths read and write.
+        n_q, n_kv, head_dim: head geometry.
+        rotary: object with cos_sin_cache ([max_pos, head_dim] bf16, cos|sin).
+        fp8: whether linears are fp8 block-quantized (bf16 linears are not
+            part of this build).
+        ue8m0: round activation scales up to powers of two (DeepGEMM's
+            UE8M0 mode); fp32 scales otherwise.
+        gemm_hook: optional callable(name, M, N, K, launch) wrapping GEMM
+            launches (bench.py times them with HIP events).
+    """
+
+    def __init__(self, arena, *, n_q, n_kv, head_dim, rotary, fp8=True,
+                 kernels_name="quail", ue8m0=False, gemm_hook=None):
+        import torch
+        if not fp8:
+            raise ValueError("this build runs fp8 block-scaled linears only")
+        if kernels_name != "quail":
+            raise ValueError(f"kernels must be 'quail', got {kernels_name!r}")
+        self.torch = torch
+        self.arena = arena
+        self.rotary = rotary
+        self.num_q_heads = n_q
+        self.num_kv_heads = n_kv
+        self.head_dim = head_dim
+        self.use_ue8m0 = bool(ue8m0)
+        self.is_fp8 = True
+        self.softmax_scale = 1.0 / math.sqrt(head_dim)
+        self.gemm_hook = gemm_hook
+
+    # ---- weights and quant ------------------------------------------
+
+    def gemm(self, q_input, input_scale, linear, name="gemm"):
+        w = linear.weight
+        launch = lambda: kernels.fp8_gemm_nt(q_input, input_scale, w, linear.weight_scale)
+        if self.gemm_hook is not None:
+            return self.gemm_hook(name, q_input.shape[0], w.shape[0], w.shape[1], launch)
+        return launch()
+
+    def quant(self, x):
+        return kernels.group_quant(x, self.use_ue8m0)
+
+    def norm_quant(self, hidden, norm, residual=None):
+        """RMS-normed, fp8-quantized GEMM input; adds the residual first when given."""
+        return kernels.add_rmsnorm_quant(hidden, norm.weight, norm.variance_epsilon,
+                                         residual=residual, ue8m0=self.use_ue8m0)
+
+    def activation_quant(self, gate_up):
+        return kernels.silu_mul_quant(gate_up, self.use_ue8m0)
+
+    def qkv_norm_rope(self, qkv, positions, attn):
+        """Normed, rotated q and k, and contiguous v, from the fused qkv output."""
+        return kernels.qk_norm_rope(
+            qkv, positions, self.rotary.cos_sin_cache, attn.q_norm.weight,
+            attn.k_norm.weight, attn.q_norm.variance_epsilon, self.num_q_heads,
+            self.num_kv_heads, self.head_dim)
+
+    def qk_norm_rope(self, qkv, positions, attn):
+        q, k, _ = self.qkv_norm_rope(qkv, positions, attn)
+        return q, k
+
+    def fused_add_rms_norm_rows(self, hidden, residual, rows, norm):
+        """Final norm of the answer rows: gather + add + RMSNorm in one kernel."""
+        return kernels.final_norm(hidden, residual, rows, norm.weight,
+                                  norm.variance_epsilon)
+
+    # ---- attention ----------------------------------------------------
+
+    def attention(self, q, k, v, chunk):
+        """Attention over the chunk and the arena; the quantized o_proj input."""
+        n = q.shape[0]
+        H, KH, D = self.num_q_heads, self.num_kv_heads, self.head_dim
+        q3 = q.view(n, H, D)
+        k3 = k.view(n, KH, D)
+        v3 = v.contiguous().view(n, KH, D)
+        if chunk.attention_mode == "tree":
+            return self.attention_tree(q3, k3, v3, chunk.meta, n)
+        return self.quant(self.attention_unified(q3, k3, v3, chunk.meta, n))
+
+    def _causal_own(self, q3, k3, v3, meta, n, want_lse):
+        """Causal attention of each packed segment over its own rows (call A)."""
+        a_len = meta["a_len"]
+        return kernels.attention(
+            q3, meta["cu_a"], a_len, n_queries=n, max_q=meta["max_a"],
+            softmax_scale=self.softmax_scale, causal=True, k_rows=k3, v_rows=v3,
+            cu_k=meta["cu_a"], n_kv=self.num_kv_heads, want_lse=want_lse)
+
+    def attention_unified(self, q3, k3, v3, meta, n):
+        layer = meta["layer"]
+        unified = meta["unified"]
+        if unified is None:
+            out, _ = self._causal_own(q3, k3, v3, meta, n, want_lse=False)
+            meta["layer"] += 1
+            return out.view(n, -1)
+        k_pool, v_pool = self.arena.layer_kv(layer)
+        kernels.kv_row_scatter(k3, v3, k_pool, v_pool, unified["src"], unified["dst"])
+        if unified["tail_src"] is not None:
+            kernels.kv_row_copy(k_pool, v_pool, unified["tail_src"], unified["tail_dst"])
+        out, _ = kernels.attention(
+            q3, unified["cu_q"], unified["used"], n_queries=n, max_q=unified["max_q"],
+            softmax_scale=self.softmax_scale, causal=True, k_pool=k_pool, v_pool=v_pool,
+            table=unified["table"], n_kv=self.num_kv_heads)
+        meta["layer"] += 1
+        return out.view(n, -1)
+
+    def attention_tree(self, q3, k3, v3, meta, n):
+        layer = meta["layer"]
+        k_pool, v_pool = self.arena.layer_kv(layer)
+        if meta["kv_src"] is not None:
+            kernels.kv_row_scatter(k3, v3, k_pool, v_pool, meta["kv_src"], meta["kv_dst"])
+        reads = meta["reads"]
+        out_a, lse_a = self._causal_own(q3, k3, v3, meta, n, want_lse=reads is not None)
+        if reads is None:
+            meta["layer"] += 1
+            return self.quant(out_a.view(n, -1))
+        out_b, lse_b = kernels.attention(
+            q3, reads["cu_q"], reads["used"], n_queries=reads["n_rows"],
+            max_q=reads["max_q"], softmax_scale=self.softmax_scale, causal=False,
+            k_pool=k_pool, v_pool=v_pool, table=reads["table"], q_rows=reads["rows"],
+            n_kv=self.num_kv_heads, want_lse=True)
+        q_out, scales = kernels.merge_attn_quant(out_a, lse_a, out_b, lse_b,
+                                                 reads["source"], self.use_ue8m0)
+        meta["layer"] += 1
+        return q_out, scales

@@ -1,0 +1,88 @@
+"""Prefix tree and sizing formulas against the reference's known answers.
+
+prefix_tree: tests/test_tokens.py:74-108 of the reference and the worked
+example of docs/content/docs/architecture/prefix-caching.mdx:38-50.
+Budgets: tests/test_specs_budgets.py:16-43 and tests/test_model_pipelines.py:
+45-58 of the reference, and the MI355X sizing they imply.
+"""
+
+from dataclasses import replace
+
+from quail_amd import budgets
+from quail_amd.specs import H100_SXM, MI355X, QWEN3_4B_FP8, QWEN3_32B_FP8
+from quail_amd.tokens import DocumentPrefixes, prefix_tree
+
+
+def test_prefix_tree_borrows_whole_pages_and_siblings_share_one_parent():
+    docs = [list(range(40)), list(range(50)), list(range(32)) + [99] * 20,
+            [7] * 20, [7] * 10]
+    tree = prefix_tree(docs, 16)
+    assert tree.order == [0, 1, 2, 4, 3]
+    assert tree.parent == [None, 0, 0, None, None]
+    assert tree.shared == [0, 32, 32, 0, 0]
+    assert tree.shared_tokens == 64
+    first = {index: pos for pos, index in enumerate(tree.order)}
+    assert all(p is None or first[p] < first[i] for i, p in enumerate(tree.parent))
+    assert prefix_tree([], 16).shared_tokens == 0
+    tree = prefix_tree([[], [], [5] * 16 + [6]], 16)
+    assert tree.parent == [None, None, None] and tree.shared == [0, 0, 0]
+
+    header = list(range(64))
+    docs = [header + [1] * 8, header + [2] * 8, header + [3] * 8,
+            header + [3] * 8 + [4] * 40, header + [5] * 8]
+    tree = prefix_tree(docs, 16)
+    assert tree.parent == [None, 0, 0, 0, 0]
+    assert tree.shared == [0, 64, 64, 64, 64]
+    docs = [header + [1] * 32, header + [1] * 32 + [2] * 8, header + [1] * 32 + [3] * 8]
+    tree = prefix_tree(docs, 16)
+    assert tree.parent == [None, 0, 0] and tree.shared == [0, 96, 96]
+
+
+def test_prefix_tree_docs_worked_example():
+    trace = list(range(2000))
+    tree = prefix_tree([trace[:1000], trace[:1400], trace[:1900]], 16)
+    assert tree.order == [0, 1, 2]
+    assert tree.parent == [None, 0, 1]
+    assert tree.shared == [0, 992, 1392]
+    computed = sum(n - s for n, s in zip((1000, 1400, 1900), tree.shared))
+    assert computed == 1000 + 408 + 508 == 1916
+
+
+def test_prefix_tree_sorts_ids_as_big_endian_int32():
+    # 256 sorts after 1 even though its low byte is 0
+    tree = prefix_tree([[256, 5], [1, 9], [255, 0]], 16)
+    assert tree.order == [1, 2, 0]
+
+
+def test_document_prefixes_prepend_the_instruction():
+    rows = DocumentPrefixes([7, 8], [[1, 2, 3], [4]])
+    assert [list(r) for r in rows] == [[7, 8, 1, 2, 3], [7, 8, 4]]
+
+
+def test_budgets_match_the_reference_on_h100_and_size_mi355x():
+    assert QWEN3_4B_FP8.head_mem_bytes == 0.0
+    assert QWEN3_32B_FP8.head_mem_bytes == 151_936 * 5_120 * 2
+    tokens = budgets.arena_tokens(QWEN3_4B_FP8, H100_SXM)
+    assert tokens == 362_240 and tokens // 16 == 22_640
+    grown = budgets.arena_tokens(QWEN3_32B_FP8, H100_SXM)
+    assert grown == 112_304
+    kept = replace(QWEN3_32B_FP8, tied_head=True)
+    assert grown - budgets.arena_tokens(kept, H100_SXM) == 5_936
+    assert budgets.kernel_index_cap(QWEN3_4B_FP8) == (2**31 - 1) // 19456 == 110_376
+    # MI355X: 288 GB HBM, 8 TB/s, fp8 5.03 PF
+    assert budgets.chunk_budget(QWEN3_4B_FP8, MI355X) == 110_376
+    assert budgets.arena_pages(QWEN3_4B_FP8, MI355X) == (106_394, 0)
+    assert budgets.chunk_budget(QWEN3_32B_FP8, MI355X) == 41_943
+    assert budgets.arena_pages(QWEN3_32B_FP8, MI355X) == (54_131, 0)
+    assert abs(QWEN3_4B_FP8.gemm_flops_per_token() - 7.2666e9) < 1e6
+
+
+def test_attention_path_choice_follows_the_roofline():
+    # C3: ~400 readers of a 64-token node with ~250 rows each: unified
+    assert budgets.choose_attention_path(QWEN3_4B_FP8, MI355X, readers=400,
+                                         reader_rows=250, node_tokens=64) == "unified"
+    # many short readers of a long node: tree
+    assert budgets.choose_attention_path(QWEN3_4B_FP8, MI355X, readers=256,
+                                         reader_rows=8, node_tokens=2048) == "tree"
+    assert budgets.choose_attention_path(QWEN3_4B_FP8, MI355X, readers=1,
+                                         reader_rows=8, node_tokens=2048) == "unified"
