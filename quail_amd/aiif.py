@@ -73,7 +73,8 @@ class FilterRunner:
     """
 
     def __init__(self, model, spec, *, device_spec=MI355X, n_pages=None, budget=None,
-                 attention_mode=None, ue8m0=False, gemm_hook=None, keep_margins=True,
+                 attention_mode=None, ue8m0=False, gemm_hook=None, attention_hook=None,
+                 keep_margins=True,
                  true_ids=SYNTHETIC_TRUE_IDS, false_ids=SYNTHETIC_FALSE_IDS):
         import torch
         self.torch = torch
@@ -85,7 +86,7 @@ class FilterRunner:
         self.arena = KVArena(n_layers, n_pages, budgets.PAGE_TOKENS, spec.n_kv,
                              spec.d_head, dtype=torch.bfloat16, device="cuda")
         self.pipeline = Qwen3Pipeline(model, self.arena, spec=spec, ue8m0=ue8m0,
-                                      gemm_hook=gemm_hook)
+                                      gemm_hook=gemm_hook, attention_hook=attention_hook)
         self.rows = AnswerRows(torch, model, true_ids, false_ids)
         self.answers = AsyncAnswers(torch, self.rows, keep_margins=keep_margins)
         self.attention_mode = attention_mode

@@ -35,10 +35,13 @@ class Engine:
             UE8M0 mode); fp32 scales otherwise.
         gemm_hook: optional callable(name, M, N, K, launch) wrapping GEMM
             launches (bench.py times them with HIP events).
+        attention_hook: optional callable(kind, pairs, kv_rows, n_queries,
+            launch) wrapping attention launches.
     """
 
     def __init__(self, arena, *, n_q, n_kv, head_dim, rotary, fp8=True,
-                 kernels_name="quail", ue8m0=False, gemm_hook=None):
+                 kernels_name="quail", ue8m0=False, gemm_hook=None,
+                 attention_hook=None):
         import torch
         if not fp8:
             raise ValueError("this build runs fp8 block-scaled linears only")
@@ -54,6 +57,7 @@ class Engine:
         self.is_fp8 = True
         self.softmax_scale = 1.0 / math.sqrt(head_dim)
         self.gemm_hook = gemm_hook
+        self.attention_hook = attention_hook
 
     # ---- weights and quant ------------------------------------------
 
@@ -104,13 +108,19 @@ class Engine:
             return self.attention_tree(q3, k3, v3, chunk.meta, n)
         return self.quant(self.attention_unified(q3, k3, v3, chunk.meta, n))
 
+    def _timed(self, kind, pairs, kv_rows, n_queries, launch):
+        if self.attention_hook is None:
+            return launch()
+        return self.attention_hook(kind, pairs, kv_rows, n_queries, launch)
+
     def _causal_own(self, q3, k3, v3, meta, n, want_lse):
         """Causal attention of each packed segment over its own rows (call A)."""
         a_len = meta["a_len"]
-        return kernels.attention(
+        work = meta.get("work", {})
+        return self._timed("own", work.get("own_pairs", 0), n, n, lambda: kernels.attention(
             q3, meta["cu_a"], a_len, n_queries=n, max_q=meta["max_a"],
             softmax_scale=self.softmax_scale, causal=True, k_rows=k3, v_rows=v3,
-            cu_k=meta["cu_a"], n_kv=self.num_kv_heads, want_lse=want_lse)
+            cu_k=meta["cu_a"], n_kv=self.num_kv_heads, want_lse=want_lse))
 
     def attention_unified(self, q3, k3, v3, meta, n):
         layer = meta["layer"]
@@ -123,10 +133,13 @@ class Engine:
         kernels.kv_row_scatter(k3, v3, k_pool, v_pool, unified["src"], unified["dst"])
         if unified["tail_src"] is not None:
             kernels.kv_row_copy(k_pool, v_pool, unified["tail_src"], unified["tail_dst"])
-        out, _ = kernels.attention(
-            q3, unified["cu_q"], unified["used"], n_queries=n, max_q=unified["max_q"],
-            softmax_scale=self.softmax_scale, causal=True, k_pool=k_pool, v_pool=v_pool,
-            table=unified["table"], n_kv=self.num_kv_heads)
+        work = meta.get("work", {})
+        out, _ = self._timed(
+            "unified", work.get("unified_pairs", 0), work.get("unified_kv_rows", 0), n,
+            lambda: kernels.attention(
+                q3, unified["cu_q"], unified["used"], n_queries=n, max_q=unified["max_q"],
+                softmax_scale=self.softmax_scale, causal=True, k_pool=k_pool,
+                v_pool=v_pool, table=unified["table"], n_kv=self.num_kv_heads))
         meta["layer"] += 1
         return out.view(n, -1)
 
@@ -140,11 +153,14 @@ class Engine:
         if reads is None:
             meta["layer"] += 1
             return self.quant(out_a.view(n, -1))
-        out_b, lse_b = kernels.attention(
-            q3, reads["cu_q"], reads["used"], n_queries=reads["n_rows"],
-            max_q=reads["max_q"], softmax_scale=self.softmax_scale, causal=False,
-            k_pool=k_pool, v_pool=v_pool, table=reads["table"], q_rows=reads["rows"],
-            n_kv=self.num_kv_heads, want_lse=True)
+        work = meta.get("work", {})
+        out_b, lse_b = self._timed(
+            "read", work.get("read_pairs", 0), work.get("read_kv_rows", 0), reads["n_rows"],
+            lambda: kernels.attention(
+                q3, reads["cu_q"], reads["used"], n_queries=reads["n_rows"],
+                max_q=reads["max_q"], softmax_scale=self.softmax_scale, causal=False,
+                k_pool=k_pool, v_pool=v_pool, table=reads["table"], q_rows=reads["rows"],
+                n_kv=self.num_kv_heads, want_lse=True))
         q_out, scales = kernels.merge_attn_quant(out_a, lse_a, out_b, lse_b,
                                                  reads["source"], self.use_ue8m0)
         meta["layer"] += 1

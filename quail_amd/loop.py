@@ -345,7 +345,22 @@ def pack_chunk(torch, arena, groups, timing=None, pinned=True, *, attention_mode
                        tail_src=staged.get("tail_src"), tail_dst=staged.get("tail_dst"),
                        used=staged["unified_used"], table=staged["unified_table"],
                        cu_q=staged["unified_cu_q"], **unified_host)
+    # attention work per layer, for throughput accounting: (query, key) pairs
+    # attended and KV rows gathered, per call
+    a_len = np.diff(np.asarray(cu_a, dtype=np.int64))
+    work = {"own_pairs": int((a_len * (a_len + 1) // 2).sum())}
+    if unified_host is not None:
+        c = np.diff(arrays["unified_cu_q"].astype(np.int64))
+        used = arrays["unified_used"].astype(np.int64)
+        work["unified_pairs"] = int((c * (used - c) + c * (c + 1) // 2).sum())
+        work["unified_kv_rows"] = int(used.sum())
+    if "reads_rows" in arrays:
+        c = np.diff(arrays["reads_cu_q"].astype(np.int64))
+        used = arrays["reads_used"].astype(np.int64)
+        work["read_pairs"] = int((c * used).sum())
+        work["read_kv_rows"] = int(used.sum())
     meta = dict(layer=0, kv_src=staged.get("kv_src"), kv_dst=staged.get("kv_dst"),
+                work=work,
                 reads=reads, unified=unified, canvas=None, cu_a=staged["cu_a"],
                 a_len=staged["a_len"],
                 max_a=max(cu_a[i + 1] - cu_a[i] for i in range(len(cu_a) - 1)))

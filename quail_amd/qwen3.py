@@ -32,7 +32,7 @@ class Qwen3Pipeline(ModelPipeline):
     """Forward passes for a Qwen3-architecture fp8 model."""
 
     def __init__(self, model, arena, *, spec=None, kernels_name="quail",
-                 engine_class=Engine, ue8m0=False, gemm_hook=None):
+                 engine_class=Engine, ue8m0=False, gemm_hook=None, attention_hook=None):
         import torch
         self.layers = model.model.layers
         self.embed = model.model.embed_tokens
@@ -42,7 +42,7 @@ class Qwen3Pipeline(ModelPipeline):
         self.engine = engine_class(arena, n_q=attn.num_heads, n_kv=attn.num_kv_heads,
                                    head_dim=attn.head_dim, rotary=attn.rotary_emb,
                                    fp8=fp8, kernels_name=kernels_name, ue8m0=ue8m0,
-                                   gemm_hook=gemm_hook)
+                                   gemm_hook=gemm_hook, attention_hook=attention_hook)
         self.tree_attention = fp8
         widest = max(max(layer.self_attn.qkv_proj.weight.shape[0],
                          layer.mlp.gate_up_proj.weight.shape[0]) for layer in self.layers)
@@ -53,15 +53,20 @@ class Qwen3Pipeline(ModelPipeline):
         return (layer.self_attn.qkv_proj, layer.self_attn.o_proj,
                 layer.mlp.gate_up_proj, layer.mlp.down_proj)
 
+    trace = None   # optional callable(layer, hidden, residual) at each layer's input
+
     def forward_chunk(self, chunk):
         """The final-normed hidden state of chunk.final_indices, [R, hidden] bf16."""
         engine = self.engine
+        trace = self.trace
         meta = chunk.meta
         meta["layer"] = 0
         positions = chunk.positions
         hidden = kernels.gather_rows(self.embed.weight, chunk.input_ids)
         residual = None
-        for layer in self.layers:
+        for index, layer in enumerate(self.layers):
+            if trace is not None:
+                trace(index, hidden, residual)
             attn = layer.self_attn
             if residual is None:
                 residual = hidden
@@ -77,6 +82,8 @@ class Qwen3Pipeline(ModelPipeline):
             gate_up = engine.gemm(g_in, g_scale, layer.mlp.gate_up_proj, "gate_up")
             d_in, d_scale = engine.activation_quant(gate_up)
             hidden = engine.gemm(d_in, d_scale, layer.mlp.down_proj, "down")
+        if trace is not None:
+            trace(len(self.layers), hidden, residual)
         return engine.fused_add_rms_norm_rows(hidden, residual, chunk.final_indices,
                                               self.final_norm)
 

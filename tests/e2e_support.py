@@ -1,0 +1,89 @@
+"""End-to-end support: run the AI.IF filter on the GPU and replay it on the oracle.
+
+The GPU run records every chunk it executed (the staged host arrays, the
+attention path, the final-normed rows and the readout margins); the
+oracle then replays the same chunks in order over its own logical arena,
+so both sides see identical packing, page tables and KV placement.
+"""
+
+import numpy as np
+import torch
+
+from oracle import forward as oracle_forward
+from quail_amd import budgets, loop
+from quail_amd.aiif import RowPrompts
+from quail_amd.model import build_random_qwen3
+from quail_amd.qwen3 import Qwen3Pipeline
+from quail_amd.readout import AnswerRows, AsyncAnswers
+from quail_amd.specs import ModelSpec
+from quail_amd.tokens import prefix_tree
+from quail_amd.arena import KVArena
+
+TINY = ModelSpec(name="qwen3-tiny", params=0.03e9, layers=2, hidden=1024, n_q=8, n_kv=2,
+                 d_head=128, ffn_width=3072, vocab=4096, tied_head=True)
+TINY_TRUE = (11, 500, 1201, 3333)
+TINY_FALSE = (12, 777, 2048, 4000)
+
+
+class Recorder:
+    """Wraps a pipeline; keeps (host arrays, path, normed rows) per chunk."""
+
+    def __init__(self, pipeline):
+        self.pipeline = pipeline
+        self.tree_attention = pipeline.tree_attention
+        self.canvas_ids = ()
+        self.needs_pages = False
+        self.records = []
+
+    def forward_chunk(self, chunk):
+        normed = self.pipeline.forward_chunk(chunk)
+        self.records.append((chunk.host, chunk.attention_mode, normed.cpu()))
+        return normed
+
+
+def gpu_filter(model, spec, docs, tail, *, path, pages, budget, true_ids, false_ids):
+    arena = KVArena(len(model.model.layers), pages, 16, spec.n_kv, spec.d_head,
+                    dtype=torch.bfloat16, device="cuda")
+    pipe = Recorder(Qwen3Pipeline(model, arena, spec=spec))
+    rows = AnswerRows(torch, model, true_ids, false_ids)
+    ans = AsyncAnswers(torch, rows, keep_margins=True)
+    stream = loop.FilterStream(torch, arena, pipe, ans, docs, [list(tail)], budget,
+                               arena_writes=True, attention_mode=path,
+                               prefix_tree=prefix_tree(docs, 16))
+    while not stream.done:
+        stream.next()
+    torch.cuda.synchronize()
+    assert not arena.accounting.owned
+    # margins per document, in the order chunks answered
+    margins = {}
+    for groups, m in zip(stream.packed_groups, ans.margins):
+        for (doc, _, _), v in zip(groups, m):
+            margins[doc] = float(v)
+    answers = {d: stream.answers[d][0] for d in range(len(docs))}
+    return answers, margins, pipe.records, stream
+
+
+def oracle_replay(model, spec, records, pages, true_ids, false_ids, gemm=None):
+    w = oracle_forward.cpu_weights(model)
+    arena = oracle_forward.OracleArena(len(w["layers"]), pages, spec.n_kv, spec.d_head)
+    gemm = gemm or oracle_forward.exact_gemm
+    outs = []
+    for host, path, _ in records:
+        normed = oracle_forward.forward_chunk(w, host, path, arena, gemm=gemm)
+        bits, margin = oracle_forward.readout(w, normed, true_ids, false_ids)
+        outs.append((normed, bits, margin))
+    return outs
+
+
+def tiny_workload(seed, n_rows, prefix=40, max_doc=150, tail_len=9, vocab=4096):
+    rng = np.random.default_rng(seed)
+    instruction = rng.integers(0, vocab, size=prefix)
+    documents = [rng.integers(0, vocab, size=int(rng.integers(1, max_doc)))
+                 for _ in range(n_rows)]
+    tail = rng.integers(0, vocab, size=tail_len)
+    return RowPrompts(instruction, documents), tail
+
+
+def tiny_model(seed=0):
+    return build_random_qwen3(TINY, seed=seed, device="cuda", max_pos=2048,
+                              answer_token_ids=TINY_TRUE + TINY_FALSE)

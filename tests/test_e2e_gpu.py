@@ -1,0 +1,203 @@
+"""End-to-end AI.IF on the GPU against the oracle (MI355X only).
+
+A random-init Qwen3-architecture fp8 model filters rows sharing a 40-token
+instruction, with a chunk budget small enough that page borrowing crosses
+chunks; the oracle replays the exact chunks the GPU ran.
+
+Dynamic 1x128 fp8 activation scales make a random model's forward chaotic
+at the percent level: a one-ulp change in a group's largest value
+re-quantizes the whole group. Two equally valid CPU restatements (fp64
+block sums vs dequantize-then-fp32 GEMM) already differ by ~0.7% per layer
+and disagree on ~1-2% of decisions, all within ~0.2 of a tie; the GPU adds
+FlashAttention's bf16 P and bf16 output rounding (~0.1% per attention
+output). The bars, written in the tests:
+  - per stage, each kernel given the GPU's own input of that stage:
+    within 1e-3 relative L2 of the oracle (2e-3 for attention's bf16 out);
+  - teacher-forced per layer (the oracle layer gets the GPU's layer input,
+    so drift cannot cascade across layers): down-projection output within
+    8% relative L2 (worst row 20%), residual stream within 2%;
+  - decisions: every row whose oracle margin exceeds 0.25 agrees, and at
+    least 95% of all rows agree.
+"""
+
+from dataclasses import replace
+
+import pytest
+import torch
+
+from e2e_support import (TINY, TINY_FALSE, TINY_TRUE, gpu_filter, tiny_workload)
+from oracle import forward as oforward
+from quail_amd import loop
+from quail_amd.arena import KVArena
+from quail_amd.model import build_random_qwen3
+from quail_amd.qwen3 import Qwen3Pipeline
+from quail_amd.readout import AnswerRows, AsyncAnswers
+from quail_amd.tokens import prefix_tree
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(x, y):
+    x, y = x.float().cpu(), y.float().cpu()
+    return ((x - y).norm() / y.norm()).item()
+
+
+@pytest.mark.parametrize("path", ["unified", "tree"])
+def test_every_layer_matches_the_oracle_teacher_forced(path):
+    spec = replace(TINY, layers=4)
+    model = build_random_qwen3(spec, seed=3, device="cuda", max_pos=2048,
+                               answer_token_ids=TINY_TRUE + TINY_FALSE)
+    docs, tail = tiny_workload(seed=4, n_rows=40)
+    pages = 240
+    arena = KVArena(spec.layers, pages, 16, spec.n_kv, spec.d_head, device="cuda")
+    pipe = Qwen3Pipeline(model, arena, spec=spec)
+    traces, hosts = [], []
+
+    def trace(layer, hidden, residual):
+        traces[-1].append((hidden.float().cpu(),
+                           None if residual is None else residual.float().cpu()))
+
+    class Rec:
+        tree_attention, canvas_ids, needs_pages = True, (), False
+
+        def forward_chunk(self, chunk):
+            traces.append([])
+            hosts.append((chunk.host, chunk.attention_mode))
+            return pipe.forward_chunk(chunk)
+
+    pipe.trace = trace
+    ans = AsyncAnswers(torch, AnswerRows(torch, model, TINY_TRUE, TINY_FALSE))
+    stream = loop.FilterStream(torch, arena, Rec(), ans, docs, [list(tail)], 1100,
+                               arena_writes=True, attention_mode=path,
+                               prefix_tree=prefix_tree(docs, 16))
+    while not stream.done:
+        stream.next()
+    assert stream.chunks >= 3 and stream.sched.borrowing.borrowed_tokens > 0
+    w = oforward.cpu_weights(model)
+    oarena = oforward.OracleArena(spec.layers, pages, spec.n_kv, spec.d_head)
+    report = []
+    for (host, mode), layers in zip(hosts, traces):
+        for li, L in enumerate(w["layers"]):
+            h_in, r_in = layers[li]
+            h_in = h_in.to(torch.bfloat16)
+            r_in = None if r_in is None else r_in.to(torch.bfloat16)
+            h_ref, r_ref = oforward.layer_step(L, li, h_in, r_in, host, mode, oarena)
+            h_gpu, r_gpu = layers[li + 1]
+            worst = ((h_gpu - h_ref.float()).norm(dim=1)
+                     / h_ref.float().norm(dim=1).clamp(min=1e-6)).max().item()
+            rec = (li, _rel(h_gpu, h_ref), worst, _rel(r_gpu, r_ref))
+            report.append(rec)
+            assert rec[1] < 0.08 and rec[2] < 0.20 and rec[3] < 0.02, f"layer {rec}"
+    print("teacher-forced (layer, hidden rel, worst row, residual rel):",
+          [tuple(round(x, 5) for x in r) for r in report[:6]])
+
+
+@pytest.mark.parametrize("path", ["unified", "tree"])
+def test_decisions_agree_outside_the_noise_band(path):
+    model = build_random_qwen3(TINY, seed=3, device="cuda", max_pos=2048,
+                               answer_token_ids=TINY_TRUE + TINY_FALSE)
+    docs, tail = tiny_workload(seed=4, n_rows=96)
+    pages = 400
+    answers, margins, records, stream = gpu_filter(
+        model, TINY, docs, tail, path=path, pages=pages, budget=2000,
+        true_ids=TINY_TRUE, false_ids=TINY_FALSE)
+    w = oforward.cpu_weights(model)
+    a1 = oforward.OracleArena(TINY.layers, pages, TINY.n_kv, TINY.d_head)
+    a2 = oforward.OracleArena(TINY.layers, pages, TINY.n_kv, TINY.d_head)
+    dequant = oforward.DequantGemm()
+    ref_bits, ref_margin, alt_bits, alt_margin = {}, {}, {}, {}
+    for (host, mode, _), groups in zip(records, stream.packed_groups):
+        n1 = oforward.forward_chunk(w, host, mode, a1)
+        n2 = oforward.forward_chunk(w, host, mode, a2, gemm=dequant)
+        b1, m1 = oforward.readout(w, n1, TINY_TRUE, TINY_FALSE)
+        b2, m2 = oforward.readout(w, n2, TINY_TRUE, TINY_FALSE)
+        for (doc, _, _), x1, y1, x2, y2 in zip(groups, b1.tolist(), m1.tolist(),
+                                               b2.tolist(), m2.tolist()):
+            ref_bits[doc], ref_margin[doc], alt_bits[doc], alt_margin[doc] = x1, y1, x2, y2
+    n = len(docs)
+    shift = max(abs(ref_margin[d] - alt_margin[d]) for d in range(n))
+    floor = sum(ref_bits[d] == alt_bits[d] for d in range(n))
+    agree = sum(answers[d] == ref_bits[d] for d in range(n))
+    for d in range(n):
+        if answers[d] != ref_bits[d]:
+            assert abs(ref_margin[d]) <= 0.25, \
+                f"row {d}: decision differs at margin {ref_margin[d]:.4f}"
+    assert agree >= 0.95 * n, f"GPU agrees on {agree}/{n}"
+    print(f"{path}: GPU-vs-oracle {agree}/{n}, oracle-vs-oracle {floor}/{n}, "
+          f"largest oracle-vs-oracle margin shift {shift:.4f}")
+
+
+def test_each_layer_stage_matches_the_oracle_on_identical_inputs():
+    import math
+    from oracle import ops
+    from quail_amd import kernels as K, layout
+    from e2e_support import tiny_model
+    model = tiny_model(seed=3)
+    docs, tail = tiny_workload(seed=4, n_rows=6)
+    arena = KVArena(2, 200, 16, TINY.n_kv, TINY.d_head, device="cuda")
+    groups = []
+    for i in range(6):
+        arena.activate(("d", i), len(docs[i]), capacity_tokens=len(docs[i]) + 9)
+        groups.append(dict(key=("d", i), prefix=docs[i], f=len(docs[i]), suffixes=[list(tail)]))
+    chunk = loop.pack_chunk(torch, arena, groups, attention_mode="unified")
+    h = chunk.host
+    L = model.model.layers[0]
+    a = L.self_attn
+    cpu = lambda t: t.cpu()
+    emb = K.gather_rows(model.model.embed_tokens.weight, chunk.input_ids)
+    assert torch.equal(cpu(emb), model.model.embed_tokens.weight.cpu()[torch.from_numpy(h["input_ids"])])
+    qi, qs = K.add_rmsnorm_quant(emb, L.input_layernorm.weight, 1e-6)
+    qr, sr = ops.norm_quant_plain(cpu(emb), cpu(L.input_layernorm.weight), 1e-6)
+    assert _rel(ops.dequant_rows(cpu(qi), cpu(qs)), ops.dequant_rows(qr, sr)) < 1e-3
+    gemm_ref = lambda x, s, lin: ops.fp8_gemm(cpu(x), cpu(s).contiguous(), cpu(lin.weight),
+                                              cpu(lin.weight_scale))
+    qkv = K.fp8_gemm_nt(qi, qs, a.qkv_proj.weight, a.qkv_proj.weight_scale)
+    assert _rel(qkv, gemm_ref(qi, qs, a.qkv_proj)) < 1e-3
+    cs = model.rotary.cos_sin_cache
+    q, k, v = K.qk_norm_rope(qkv, chunk.positions, cs, a.q_norm.weight, a.k_norm.weight,
+                             1e-6, 8, 2, 128)
+    q2, k2, v2 = ops.qk_norm_rope(cpu(qkv), torch.from_numpy(h["positions"]), cpu(cs),
+                                  cpu(a.q_norm.weight), cpu(a.k_norm.weight), 1e-6, 8, 2, 128)
+    assert _rel(q, q2) < 1e-3 and _rel(k, k2) < 1e-3 and torch.equal(cpu(v), v2)
+    T = q.shape[0]
+    u = chunk.meta["unified"]
+    kp, vp = arena.layer_kv(0)
+    K.kv_row_scatter(k.view(T, 2, 128), v.view(T, 2, 128), kp, vp, u["src"], u["dst"])
+    out, _ = K.attention(q.view(T, 8, 128), u["cu_q"], u["used"], n_queries=T,
+                         max_q=u["max_q"], softmax_scale=1 / math.sqrt(128), causal=True,
+                         k_pool=kp, v_pool=vp, table=u["table"], n_kv=2)
+    out_ref, _ = ops.paged_attention(cpu(q).view(T, 8, 128), layout.k_rows(cpu(kp)),
+                                     layout.v_rows(cpu(vp)),
+                                     torch.from_numpy(h["unified_cu_q"]),
+                                     torch.from_numpy(h["unified_used"]),
+                                     torch.from_numpy(h["unified_table"]),
+                                     1 / math.sqrt(128), True)
+    assert _rel(out, out_ref) < 2e-3
+    oq, os_ = K.group_quant(out.view(T, -1))
+    hid = K.fp8_gemm_nt(oq, os_, a.o_proj.weight, a.o_proj.weight_scale)
+    assert _rel(hid, gemm_ref(oq, os_, a.o_proj)) < 1e-3
+    res = emb.clone()
+    gq, gs = K.add_rmsnorm_quant(hid, L.post_attention_layernorm.weight, 1e-6, residual=res)
+    gqr, gsr, resr = ops.add_rms_norm_quant(cpu(hid), cpu(emb), cpu(L.post_attention_layernorm.weight), 1e-6)
+    assert torch.equal(cpu(res), resr)
+    assert _rel(ops.dequant_rows(cpu(gq), cpu(gs)), ops.dequant_rows(gqr, gsr)) < 1e-3
+    gu = K.fp8_gemm_nt(gq, gs, L.mlp.gate_up_proj.weight, L.mlp.gate_up_proj.weight_scale)
+    assert _rel(gu, gemm_ref(gq, gs, L.mlp.gate_up_proj)) < 1e-3
+    dq, ds = K.silu_mul_quant(gu)
+    dqr, dsr = ops.silu_mul_quant(cpu(gu))
+    assert _rel(ops.dequant_rows(cpu(dq), cpu(ds)), ops.dequant_rows(dqr, dsr)) < 1e-3
+    dn = K.fp8_gemm_nt(dq, ds, L.mlp.down_proj.weight, L.mlp.down_proj.weight_scale)
+    assert _rel(dn, gemm_ref(dq, ds, L.mlp.down_proj)) < 1e-3
+
+
+def test_unified_and_tree_paths_agree_on_the_gpu():
+    model = build_random_qwen3(TINY, seed=5, device="cuda", max_pos=2048,
+                               answer_token_ids=TINY_TRUE + TINY_FALSE)
+    docs, tail = tiny_workload(seed=6, n_rows=32)
+    a, ma, _, _ = gpu_filter(model, TINY, docs, tail, path="unified", pages=160,
+                             budget=900, true_ids=TINY_TRUE, false_ids=TINY_FALSE)
+    b, mb, _, _ = gpu_filter(model, TINY, docs, tail, path="tree", pages=160,
+                             budget=900, true_ids=TINY_TRUE, false_ids=TINY_FALSE)
+    for d in range(len(docs)):
+        if a[d] != b[d]:
+            assert abs(ma[d]) <= 0.25 and abs(mb[d]) <= 0.25, f"row {d}"
