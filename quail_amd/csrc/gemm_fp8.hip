@@ -22,6 +22,7 @@ namespace qh {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 namespace gemm {
 constexpr int BM = 256, BN = 256, BK = 128;
@@ -32,11 +33,13 @@ constexpr int XCDS = 8;
 }  // namespace gemm
 
 
-// LDS rows hold their eight 16-byte chunks XOR-swizzled by (row / 2) % 8:
-// the 16 lanes of one fragment read (16 consecutive rows, one logical chunk)
-// then hit 16 distinct 4-bank groups.
+// LDS rows hold their eight 16-byte chunks XOR-swizzled by row % 8. A
+// fragment read (16 consecutive rows; lane group g = lane/16 reads logical
+// chunks g and g+4) is then free of bank conflicts on gfx950's 64-bank LDS,
+// as measured with a ds_read_b128 probe over candidate patterns (a
+// (row / 2) % 8 swizzle runs at half rate).
 __device__ __forceinline__ int swz(int row, int chunk) {
-  return chunk ^ ((row >> 1) & 7);
+  return chunk ^ (row & 7);
 }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -153,12 +156,13 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_nt_kernel(
                                                 rsa, srow[j], kboff, 0));
   };
 
-  // Fragment reads: lane reads row base + 16*t + lane%16, logical chunks 2g and
-  // 2g+1. For every such row (row / 2) % 8 == (lane % 16) / 2, so the swizzle
-  // is per lane and the rows differ by immediate offsets of 16 * 128 bytes.
-  const int sw = (lane & 15) >> 1;
-  const int frag_lo = (lane & 15) * ROW + (((2 * g) ^ sw) * 16);
-  const int frag_hi = (lane & 15) * ROW + (((2 * g + 1) ^ sw) * 16);
+  // Fragment reads: lane reads row base + 16*t + lane%16, logical chunks g and
+  // g+4 (K bytes [16g, 16g+16) and [64+16g, 64+16g+16) - both operands use the
+  // same K order, so the MFMA sums the same products). For every such row
+  // row % 8 == lane % 8, so the swizzle is per lane and the rows differ by
+  // immediate offsets of 16 * 128 bytes.
+  const int frag_lo = (lane & 15) * ROW + ((g ^ (lane & 7)) * 16);
+  const int frag_hi = (lane & 15) * ROW + (((g + 4) ^ (lane & 7)) * 16);
   auto frag = [&](const uint8_t* tile, int row16) {
     const uint8_t* p = tile + row16 * 16 * ROW;
     uint4 lo = *reinterpret_cast<const uint4*>(p + frag_lo);
@@ -234,8 +238,11 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_nt_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int n = n0 + 128 * wn + 16 * i + 4 * g;
-      const uint32_t w0 = f32_to_bf16(acc[i][j][0]) | (f32_to_bf16(acc[i][j][1]) << 16);
-      const uint32_t w1 = f32_to_bf16(acc[i][j][2]) | (f32_to_bf16(acc[i][j][3]) << 16);
+      // v_cvt_pk_bf16_f32: round-to-nearest-even, as f32_to_bf16
+      const bf16x2 p0 = {(__bf16)acc[i][j][0], (__bf16)acc[i][j][1]};
+      const bf16x2 p1 = {(__bf16)acc[i][j][2], (__bf16)acc[i][j][3]};
+      const uint32_t w0 = __builtin_bit_cast(uint32_t, p0);
+      const uint32_t w1 = __builtin_bit_cast(uint32_t, p1);
       *reinterpret_cast<uint2*>(C + (long)m * ldc + n) = make_uint2(w0, w1);
     }
   }
