@@ -224,7 +224,8 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(k["gemm_tflops"], 1),
                      "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(k["gemm_tflops"] / FP8_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "qh fp8_gemm_nt_kernel (all four Qwen3 projections)"},
+                     "kernel": ("qh fp8_gemm_kernel: qkv, o, down (bf16 out) and gate_up "
+                                "(fused SiLU gate + fp8 quant epilogue)")},
         "gemm": {"share_of_step": round(k["gemm_ms"] / (ms_per_step * args.steps), 3),
                  "shapes": k["gemm_shapes"]},
         "attention": {"tflops": round(k["attn_tflops"], 1),

@@ -95,6 +95,25 @@ int qh_fp8_gemm_nt(const void* A, long lda, const float* sa, const void* B,
                    int K, qh_stream_t stream);
 
 /*
+ * The gate_up projection fused with the SiLU-gated product and its 1x128 fp8
+ * quantization: replaces Engine.gemm(gate_up_proj) followed by
+ * Engine.activation_quant (models/qwen3.py:113-116 -> attention.py:129-141,
+ * :771-775, :300-323). B holds the gate rows [0, I) then the up rows
+ * [I, 2I) (the vLLM merged layout, unchanged). Per output column j:
+ *   g = bf16(gemm[m, j]); u = bf16(gemm[m, I + j]); y = g * sigmoid(g) * u
+ * in fp32, then quantized per 1x128 group exactly as qh_silu_mul_quant does
+ * on the bf16 gate_up tensor, so the result is bit-identical to the
+ * unfused pair.
+ *   A [M, K] e4m3 (lda); sa [K/128, M];  B [2I, K] e4m3 (ldb); sb [2I/128, K/128]
+ *   out_q [M, I] e4m3 row stride ld_out; scales [I/128, M]
+ * I must be a multiple of 128, K of 128.
+ */
+int qh_fp8_gemm_silu_quant(const void* A, long lda, const float* sa,
+                           const void* B, long ldb, const float* sb, int M,
+                           int I, int K, void* out_q, long ld_out,
+                           float* scales, int ue8m0, qh_stream_t stream);
+
+/*
  * Per-head RMSNorm of q and k, then NeoX rotary on the two 64-column halves,
  * plus a contiguous copy of v. Replaces Engine.qk_norm_rope
  * (attention.py:777-781 -> Triton qk_norm_rope :361-409) and the v

@@ -35,6 +35,8 @@ SIGNATURES = {
     "qh_add_rmsnorm_quant": [_p, _l, _p, _l, _p, _f, _i, _i, _p, _p, _i, _p],
     "qh_group_quant": [_p, _l, _i, _i, _p, _p, _i, _p],
     "qh_fp8_gemm_nt": [_p, _l, _p, _p, _l, _p, _p, _l, _i, _i, _i, _p],
+    "qh_fp8_gemm_silu_quant": [_p, _l, _p, _p, _l, _p, _i, _i, _i, _p, _l, _p,
+                               _i, _p],
     "qh_qk_norm_rope": [_p, _l, _p, _p, _i, _p, _p, _f, _i, _i, _i, _i,
                         _p, _p, _p, _p],
     "qh_kv_row_scatter": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p],

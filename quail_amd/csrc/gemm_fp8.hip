@@ -1,251 +1,447 @@
 // FP8 (OCP e4m3) block-scaled GEMM on gfx950 MFMA:
 //   C[m, n] = sum_kb sa[kb, m] * sb[n/128, kb] * sum_{k in kb} A[m, k] * B[n, k]
 // with A = activations [M, K] (1x128 per-token scales, column-major storage)
-// and B = weights [N, K] (128x128 block scales), fp32 accumulation, bf16 out.
+// and B = weights [N, K] (128x128 block scales), fp32 accumulation. Two
+// epilogues: bf16 C, or (gate_up projection) y = silu(gate) * up over the two
+// halves of B's rows, quantized per 1x128 group to e4m3 + fp32 scales.
 //
 // One v_mfma_scale_f32_16x16x128_f8f6f4 consumes exactly one 128-deep K block,
 // so each MFMA starts from zero and its 16x16 result is promoted into the fp32
 // accumulator with the block's combined scale (one FMA per output) - the
 // per-block scales never have to be powers of two. The MFMA computes
 // C^T = B A^T: its row operand is the weight tile, so a lane's four outputs are
-// four consecutive n of one m (8-byte bf16 stores) and the activation scale is
-// one value per lane.
+// four consecutive n of one m and the activation scale is one value per lane.
 //
-// Workgroup tile 256 x 256 x 128 with 8 waves (4 along M x 2 along N, 64 x 128
-// per wave). Operand tiles move global -> LDS by DMA (no staging registers)
-// into two LDS stages of 2 x 32 KiB; the next K block's DMA and scales are in
-// flight while the current block computes; one barrier per K block. Tiles are
-// mapped so that each XCD's L2 sees a contiguous group of them.
+// Structure (one workgroup of 8 waves per CU, persistent):
+//   - tile = 256 tokens x 256 weight rows (two 128-row blocks). Wave w owns
+//     tokens 32w .. 32w+31 and all 256 weight rows, so a token's whole output
+//     row segment lives in one wave (what the fused SiLU epilogue needs).
+//   - the workgroup walks its tiles as one stream of 128-deep K steps. Weight
+//     blocks reach LDS by DMA (buffer_load ... lds) NS-1 = 3 steps ahead into a
+//     4-stage ring; each wave loads its own activation fragments and the
+//     scales straight into VGPRs PA = 2 steps ahead. Loads cross tile
+//     boundaries, so a tile's first blocks arrive during the previous tile.
+//   - every wave issues exactly LOADS = 12 vector-memory loads per step, all
+//     as inline asm, one between consecutive MFMA pairs; the wait at the top
+//     of step s is vmcnt(12): the loads issued since step s's activations
+//     are exactly the previous step's twelve. The count ignores the stores
+//     of an epilogue in between: stores may complete out of order with
+//     loads, and counting only loads stays correct either way (it can only
+//     wait longer, for stores issued at the end of the step before).
+//   - one barrier per step: it publishes stage s (every wave's DMA share has
+//     landed) and frees stage s-1 for the DMA of step s+3. The first two
+//     weight fragments of step s+1 are read at the end of step s.
+//   - tiles are ordered so each XCD's L2 works on a contiguous group of them.
 #include "common.h"
+
+#include <type_traits>
 
 namespace qh {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 namespace gemm {
-constexpr int BM = 256, BN = 256, BK = 128;
-constexpr int ROW = BK;                  // LDS row: 128 fp8 bytes, no padding
-constexpr int TILE_BYTES = 256 * ROW;    // one operand, one stage: 32 KiB
+constexpr int BM = 256;         // tile tokens
+constexpr int BR = 256;         // tile weight rows
+constexpr int BK = 128;         // K block: one MFMA, one scale block
+constexpr int NS = 4;           // weight stages in LDS
+constexpr int PA = 2;           // activation blocks in flight ahead
+constexpr int STAGE = BR * BK;  // 32 KiB
+constexpr int LOADS = 12;       // vector-memory loads per wave per step
 constexpr int GROUP_M = 8;
 constexpr int XCDS = 8;
+enum { kStoreBf16 = 0, kSiluQuant = 1 };
 }  // namespace gemm
 
+struct GemmArgs {
+  const uint8_t* A;
+  long lda;
+  const float* sa;
+  const uint8_t* B;
+  long ldb;
+  const float* sb;
+  void* C;        // bf16 [M, N] (kStoreBf16) or e4m3 [M, N/2] (kSiluQuant)
+  long ldc;       // elements of C's type
+  float* scales;  // kSiluQuant: [N/256, M]
+  int M, N, K;
+  int ue8m0;
+};
 
-// LDS rows hold their eight 16-byte chunks XOR-swizzled by row % 8. A
-// fragment read (16 consecutive rows; lane group g = lane/16 reads logical
-// chunks g and g+4) is then free of bank conflicts on gfx950's 64-bank LDS,
-// as measured with a ds_read_b128 probe over candidate patterns (a
-// (row / 2) % 8 swizzle runs at half rate).
-__device__ __forceinline__ int swz(int row, int chunk) {
-  return chunk ^ (row & 7);
-}
-
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-
-// Raw buffer descriptor over a tile's rows (byte-addressed, stride 0; the
-// range check is left open because the caller clamps row indices).
-__device__ __forceinline__ i32x4 tile_rsrc(const uint8_t* base) {
+// Raw buffer descriptor: byte-addressed, `bytes` long; accesses past the end
+// read zero / are dropped.
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
   const uint64_t b = (uint64_t)base;
-  return (i32x4){(int)(uint32_t)b, (int)(uint32_t)(b >> 32), 0x7fffffff, 0x00020000};
+  return (i32x4){(int)(uint32_t)b, (int)(uint32_t)(b >> 32), (int)bytes, 0x00020000};
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// Per-lane byte offsets of the four DMA rows a lane fetches in one K block of
-// a 256-row operand tile. Wave instruction i fills the contiguous 1 KiB LDS
-// block blk = 8*i + wave (8 rows); lane l writes its 16 bytes at 16*l of it,
-// i.e. row 8*blk + l/8, physical chunk l%8, which holds logical chunk
-// swz(row, l%8) of that row.
-__device__ __forceinline__ void tile_offsets(long ld, int row0, int row_max, int wave,
-                                             int lane, uint32_t off[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = (8 * i + wave) * 8 + (lane >> 3);
-    const int grow = min(row0 + r, row_max);
-    off[i] = (uint32_t)(grow - row0) * (uint32_t)ld + (uint32_t)(swz(r, lane & 7) * 16);
-  }
+// silu(gate) * up of one GEMM output pair, with both rounded to bf16 first:
+// the same arithmetic as silu_mul_quant_kernel on a bf16 gate_up tensor.
+__device__ __forceinline__ float silu_mul_bf16(float gate_acc, float up_acc) {
+#pragma clang fp contract(off)
+  const float gate = round_bf16(gate_acc);
+  const float up = round_bf16(up_acc);
+  const float sig = 1.0f / (1.0f + expf(-gate));
+  return gate * sig * up;
 }
 
-// One K block (bytes k0 .. k0+127 of each row) global -> LDS with
-// buffer_load_dwordx4 ... lds (M0 = LDS block base). Issued as inline asm so
-// the compiler does not treat the LDS reads of the other stage as dependent
-// on it; the consumer waits with s_waitcnt vmcnt(0) + a barrier.
-__device__ __forceinline__ void load_tile_lds(i32x4 rsrc, const uint32_t off[4], uint32_t k0,
-                                              const uint8_t* tile, int wave) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t dst = lds_addr(tile + (8 * i + wave) * 1024);
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "buffer_load_dwordx4 %1, %2, %3 offen lds"
-        :
-        : "s"(dst), "v"(off[i]), "s"(rsrc), "s"(k0)
-        : "memory", "m0");
-  }
-}
-
-__global__ __launch_bounds__(512, 1) void fp8_gemm_nt_kernel(
-    const uint8_t* __restrict__ A, long lda, const float* __restrict__ sa,
-    const uint8_t* __restrict__ B, long ldb, const float* __restrict__ sb,
-    uint16_t* __restrict__ C, long ldc, int M, int N, int K) {
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
   using namespace gemm;
-  // [stage][A | B][256 rows x 128 B]
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const int wm = wave & 3, wn = wave >> 2;
-
-  // ---- tile mapping: XCD-contiguous, then grouped along M -----------------
-  const int tiles_m = (M + BM - 1) / BM;
-  const int tiles_n = N / BN;
-  const int n_tiles = tiles_m * tiles_n;
-  int pid = blockIdx.x;
-  {
-    const int per_xcd = n_tiles / XCDS;
-    if (pid < per_xcd * XCDS) pid = (pid % XCDS) * per_xcd + pid / XCDS;
-  }
-  const int in_group = GROUP_M * tiles_n;
-  const int group = pid / in_group;
-  const int first_m = group * GROUP_M;
-  const int gsize = min(tiles_m - first_m, GROUP_M);
-  const int tm = first_m + (pid % in_group) % gsize;
-  const int tn = (pid % in_group) / gsize;
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int nk = K / BK;
-
-  f32x4 acc[8][4];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  // activation-scale offsets (bytes) of the rows this lane's outputs belong
-  // to, one per m-tile; rows past M read row M-1 (their outputs are dropped)
-  uint32_t srow[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) srow[j] = 4u * min(m0 + 64 * wm + 16 * j + (lane & 15), M - 1);
-  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)sa, 0, 0x7fffffff, 0x00020000);
-  const int nblk = (n0 + 128 * wn) / 128;
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   const int g = lane >> 4;
-  const i32x4 ra = tile_rsrc(A + (long)m0 * lda);
-  const i32x4 rb = tile_rsrc(B + (long)n0 * ldb);
-  uint32_t offa[4], offb[4];
-  tile_offsets(lda, m0, M - 1, wave, lane, offa);
-  tile_offsets(ldb, n0, N - 1, wave, lane, offb);
+  const int M = p.M;
+  const int nk = p.K / BK;
+  const long lda = p.lda, ldb = p.ldb;
 
+  // ---- tiles of this workgroup --------------------------------------------
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = p.N / BR;
+  const int n_tiles = tiles_m * tiles_n;
+  const int per_xcd = n_tiles / XCDS;
+  const int G = gridDim.x;
+  const int my_tiles = (n_tiles - (int)blockIdx.x + G - 1) / G;
 
-  // Scales: s_cur holds this K block's combined per-lane scales; the next
-  // block's raw activation scales and weight scale are loaded one step ahead
-  // and only multiplied when they become current, so their loads never make
-  // the compiler wait in the middle of a step.
-  float s_cur[4], sa_nxt[4], sb_nxt;
-  auto load_scales = [&](int kb) {
-    sb_nxt = sb[(long)nblk * nk + kb];
-    const uint32_t kboff = 4u * (uint32_t)kb * (uint32_t)M;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      sa_nxt[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                rsa, srow[j], kboff, 0));
+  // linear tile t -> (tile row, tile column): XCD-contiguous chunks, then
+  // GROUP_M tile rows per column sweep
+  auto coords = [&](int t, int& tm, int& tn) __attribute__((always_inline)) {
+    if (t < per_xcd * XCDS) t = (t % XCDS) * per_xcd + t / XCDS;
+    const int in_group = GROUP_M * tiles_n;
+    const int first_m = (t / in_group) * GROUP_M;
+    const int gsize = min(tiles_m - first_m, GROUP_M);
+    tm = first_m + (t % in_group) % gsize;
+    tn = (t % in_group) / gsize;
+  };
+  // first weight row of 128-row half h of tile column tn
+  auto weight_row = [&](int tn, int h) __attribute__((always_inline)) {
+    return EPI == kSiluQuant ? h * (p.N / 2) + 128 * tn : 256 * tn + 128 * h;
   };
 
-  // Fragment reads: lane reads row base + 16*t + lane%16, logical chunks g and
-  // g+4 (K bytes [16g, 16g+16) and [64+16g, 64+16g+16) - both operands use the
-  // same K order, so the MFMA sums the same products). For every such row
-  // row % 8 == lane % 8, so the swizzle is per lane and the rows differ by
-  // immediate offsets of 16 * 128 bytes.
-  const int frag_lo = (lane & 15) * ROW + ((g ^ (lane & 7)) * 16);
-  const int frag_hi = (lane & 15) * ROW + (((g + 4) ^ (lane & 7)) * 16);
-  auto frag = [&](const uint8_t* tile, int row16) {
-    const uint8_t* p = tile + row16 * 16 * ROW;
-    uint4 lo = *reinterpret_cast<const uint4*>(p + frag_lo);
-    uint4 hi = *reinterpret_cast<const uint4*>(p + frag_hi);
-    return (v8i){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                 (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  // A position in the step stream; advancing past the last step stays there
+  // (the loads of those steps are repeats nobody reads).
+  struct Cursor {
+    int tl, kb, tm, tn;
+  };
+  auto start = [&](Cursor& c) __attribute__((always_inline)) {
+    c.tl = 0;
+    c.kb = 0;
+    coords((int)blockIdx.x, c.tm, c.tn);
+  };
+  auto advance = [&](Cursor& c) __attribute__((always_inline)) {
+    if (++c.kb == nk) {
+      if (c.tl + 1 < my_tiles) {
+        c.kb = 0;
+        ++c.tl;
+        coords((int)blockIdx.x + c.tl * G, c.tm, c.tn);
+      } else {
+        c.kb = nk - 1;
+      }
+    }
   };
 
-  // One K block from LDS stage (la, lb): 32 MFMAs, each promoted into acc one
-  // MFMA later (the promotion of (i, j) is issued behind the MFMA of the next
-  // pair, so no FMA stalls on the MFMA it reads). Two weight fragments are
-  // live at a time: the scheduler is fenced per n-tile to keep it that way.
-  auto compute = [&](const uint8_t* la, const uint8_t* lb) {
-    v8i xf[4];
+  // ---- loads ----------------------------------------------------------------
+  // Weight DMA: instruction i (0..3) fills LDS block 8*i + wave of the stage,
+  // i.e. tile rows 64*i + 8*wave + lane/8 (half i/2); lane l writes physical
+  // chunk l%8 of its row, which holds logical chunk (l%8) ^ (row%8).
+  const i32x4 rb = buffer_rsrc(p.B, (uint32_t)((long)p.N * ldb));
+  const uint32_t offb = (uint32_t)(8 * wave + (lane >> 3)) * (uint32_t)ldb +
+                        (uint32_t)((((lane & 7) ^ (lane >> 3)) & 7) * 16);
+  auto dma = [&](const Cursor& c, int stage, int i) __attribute__((always_inline)) {
+    const uint32_t dst = lds_addr(lds + stage * STAGE + (8 * i + wave) * 1024);
+    const uint32_t so = (uint32_t)(weight_row(c.tn, i >> 1) + 64 * (i & 1)) * (uint32_t)ldb +
+                        (uint32_t)c.kb * BK;
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "buffer_load_dwordx4 %1, %2, %3 offen lds"
+        :
+        : "s"(dst), "v"(offb), "s"(rb), "s"(so)
+        : "memory", "m0");
+  };
+
+  // Activation fragments: lane reads token 32*wave + 16*j + lane%16 of the
+  // tile, K bytes [16g, 16g+16) and [64+16g, 64+16g+16) of the block (the
+  // weight fragments use the same K order). Tokens past M lie outside the
+  // descriptor and read zero. Then the two activation scales of the lane's
+  // tokens and the two weight-block scales of the tile.
+  const uint32_t offa = (uint32_t)(32 * wave + (lane & 15)) * (uint32_t)lda + 16u * g;
+  const uint32_t srow = 4u * (uint32_t)(32 * wave + (lane & 15));
+  const i32x4 rsa = buffer_rsrc(p.sa, (uint32_t)nk * (uint32_t)M * 4u);
+  const i32x4 rsb = buffer_rsrc(p.sb, (uint32_t)(p.N / 128) * (uint32_t)nk * 4u);
+  struct ALoad {
+    i32x4 ra;
+    uint32_t k0, k1, ks, kw0, kw1;
+  };
+  auto a_args = [&](const Cursor& c) __attribute__((always_inline)) {
+    ALoad L;
+    const int m0 = c.tm * BM;
+    L.ra = buffer_rsrc(p.A + (long)m0 * lda, (uint32_t)((long)min(M - m0, BM) * lda));
+    L.k0 = (uint32_t)c.kb * BK;
+    L.k1 = L.k0 + 16u * (uint32_t)lda;
+    L.ks = ((uint32_t)c.kb * (uint32_t)M + (uint32_t)m0) * 4u;
+    L.kw0 = ((uint32_t)(weight_row(c.tn, 0) / 128) * (uint32_t)nk + (uint32_t)c.kb) * 4u;
+    L.kw1 = ((uint32_t)(weight_row(c.tn, 1) / 128) * (uint32_t)nk + (uint32_t)c.kb) * 4u;
+    return L;
+  };
+  auto a_load = [&](const ALoad& L, int op, i32x4* lo, i32x4* hi, float* sv, float* wv) __attribute__((always_inline)) {
+    switch (op) {
+      case 0:
+        asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen"
+                     : "=v"(lo[0]) : "v"(offa), "s"(L.ra), "s"(L.k0) : "memory");
+        break;
+      case 1:
+        asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen offset:64"
+                     : "=v"(hi[0]) : "v"(offa), "s"(L.ra), "s"(L.k0) : "memory");
+        break;
+      case 2:
+        asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen"
+                     : "=v"(lo[1]) : "v"(offa), "s"(L.ra), "s"(L.k1) : "memory");
+        break;
+      case 3:
+        asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen offset:64"
+                     : "=v"(hi[1]) : "v"(offa), "s"(L.ra), "s"(L.k1) : "memory");
+        break;
+      case 4:
+        asm volatile("buffer_load_dword %0, %1, %2, %3 offen"
+                     : "=v"(sv[0]) : "v"(srow), "s"(rsa), "s"(L.ks) : "memory");
+        break;
+      case 5:
+        asm volatile("buffer_load_dword %0, %1, %2, %3 offen offset:64"
+                     : "=v"(sv[1]) : "v"(srow), "s"(rsa), "s"(L.ks) : "memory");
+        break;
+      case 6:
+        asm volatile("buffer_load_dword %0, off, %1, %2"
+                     : "=v"(wv[0]) : "s"(rsb), "s"(L.kw0) : "memory");
+        break;
+      case 7:
+        asm volatile("buffer_load_dword %0, off, %1, %2"
+                     : "=v"(wv[1]) : "s"(rsb), "s"(L.kw1) : "memory");
+        break;
+    }
+  };
+
+  // Weight fragment (n-tile i of a stage): lane reads row 16*i + lane%16,
+  // logical chunks g and g+4; row % 8 == lane % 8, so the swizzle is per lane.
+  const int frow = (lane & 15) * BK;
+  const int c_lo = ((g ^ (lane & 7)) & 7) * 16;
+  const int c_hi = (((g + 4) ^ (lane & 7)) & 7) * 16;
+  auto frag = [&](const uint8_t* st, int i) __attribute__((always_inline)) {
+    const uint8_t* q = st + i * 16 * BK + frow;
+    const i32x4 lo = *reinterpret_cast<const i32x4*>(q + c_lo);
+    const i32x4 hi = *reinterpret_cast<const i32x4*>(q + c_hi);
+    return (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+
+  // ---- state ------------------------------------------------------------------
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[16][2];  // [n-tile][token half]
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xf[j] = frag(la, 4 * wm + j);
-    v8i wf = frag(lb, 8 * wn);
-    f32x4 tp = zero;
+  for (int i = 0; i < 16; ++i)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      v8i wf_n = wf;
-      if (i < 7) wf_n = frag(lb, 8 * wn + i + 1);
+    for (int j = 0; j < 2; ++j) acc[i][j] = zero;
+  i32x4 alo[PA + 1][2], ahi[PA + 1][2];
+  float sav[PA + 1][2], sbv[PA + 1][2];
+
+  // ---- epilogues --------------------------------------------------------------
+  auto store_bf16 = [&](const Cursor& c) __attribute__((always_inline)) {
+    uint16_t* C = (uint16_t*)p.C;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
+      const int m = c.tm * BM + 32 * wave + 16 * j + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        // v_cvt_pk_bf16_f32: round-to-nearest-even, as f32_to_bf16
+        const bf16x2 p0 = {(__bf16)acc[i][j][0], (__bf16)acc[i][j][1]};
+        const bf16x2 p1 = {(__bf16)acc[i][j][2], (__bf16)acc[i][j][3]};
+        if (m < M) {
+          const int n = c.tn * BR + 16 * i + 4 * g;
+          *reinterpret_cast<uint2*>(C + (long)m * p.ldc + n) =
+              make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
+        }
+        acc[i][j] = zero;
+      }
+    }
+  };
+  // silu(gate) * up for the tile's 128 output columns 128*tn .. (n-tiles 0-7
+  // hold gate, 8-15 the matching up), one 1x128 quantization group per token:
+  // a token's 128 values sit in the four lanes lane%16 + 16*g'.
+  auto store_silu_quant = [&](const Cursor& c) __attribute__((always_inline)) {
+    uint8_t* out = (uint8_t*)p.C;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int m = c.tm * BM + 32 * wave + 16 * j + (lane & 15);
+      float amax = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float y = silu_mul_bf16(acc[i][j][r], acc[i + 8][j][r]);
+          acc[i][j][r] = y;
+          amax = fmaxf(amax, fabsf(y));
+        }
+      amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
+      amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
+      const float scale = group_scale(amax, p.ue8m0 != 0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w |= quant_e4m3(acc[i][j][r], scale) << (8 * r);
+        if (m < M)
+          *reinterpret_cast<uint32_t*>(out + (long)m * p.ldc + 128 * c.tn + 16 * i + 4 * g) = w;
+        acc[i][j] = zero;
+        acc[i + 8][j] = zero;
+      }
+      if (g == 0 && m < M) p.scales[(long)c.tn * M + m] = scale;
+    }
+  };
+  auto epilogue = [&](const Cursor& c) __attribute__((always_inline)) {
+    if constexpr (EPI == kSiluQuant) store_silu_quant(c);
+    else store_bf16(c);
+  };
+
+  // ---- prologue: weight stages 0 .. NS-2, activation blocks 0 .. PA-1 ---------
+  Cursor cd, ca, cc;  // DMA (step s+NS-1), activations (s+PA), compute (s)
+  start(cd);
+  start(ca);
+  start(cc);
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma(cd, s, i);
+    advance(cd);
+  }
+#pragma unroll
+  for (int s = 0; s < PA; ++s) {
+    const ALoad L = a_args(ca);
+#pragma unroll
+    for (int op = 0; op < 8; ++op) a_load(L, op, alo[s], ahi[s], sav[s], sbv[s]);
+    advance(ca);
+  }
+  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // all but block 1's eight
+  __builtin_amdgcn_s_barrier();
+
+  // carried across steps: the next two weight fragments, and the last product
+  // of the previous step with its scale
+  v8i bf = frag(lds, 0), bn = frag(lds, 1);
+  f32x4 tp = zero;
+  float s_last = 0.f;
+
+  auto step = [&](auto slot_c, int s) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_c)::value;
+    constexpr int nslot = (slot + PA) % (PA + 1);
+    // step s's activations and scales (issued at step s-2) have landed, and
+    // with them this wave's DMA share of stage s (issued at s-3); the twelve
+    // loads of step s-1 may be in flight
+    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    asm volatile(""
+                 : "+v"(alo[slot][0]), "+v"(alo[slot][1]), "+v"(ahi[slot][0]),
+                   "+v"(ahi[slot][1]), "+v"(sav[slot][0]), "+v"(sav[slot][1]),
+                   "+v"(sbv[slot][0]), "+v"(sbv[slot][1]));
+    __builtin_amdgcn_s_barrier();
+    const ALoad L = a_args(ca);
+    const int dstage = (s + NS - 1) % NS;
+    float sc[2][2];  // [token half][weight half]
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      sc[j][0] = sav[slot][j] * sbv[slot][0];
+      sc[j][1] = sav[slot][j] * sbv[slot][1];
+    }
+    const uint8_t* st = lds + (s % NS) * STAGE;
+    const uint8_t* st_next = lds + ((s + 1) % NS) * STAGE;
+    const v8i xa[2] = {
+        (v8i){alo[slot][0][0], alo[slot][0][1], alo[slot][0][2], alo[slot][0][3],
+              ahi[slot][0][0], ahi[slot][0][1], ahi[slot][0][2], ahi[slot][0][3]},
+        (v8i){alo[slot][1][0], alo[slot][1][1], alo[slot][1][2], alo[slot][1][3],
+              ahi[slot][1][0], ahi[slot][1][1], ahi[slot][1][2], ahi[slot][1][3]}};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      // fragments two n-tiles ahead; the last two are step s+1's first, from
+      // a stage the wait and barrier above already covered
+      const v8i bnn = i < 14 ? frag(st, i + 2) : frag(st_next, i - 14);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
         const f32x4 t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            wf, xf[j], zero, 0, 0, 0, 127, 0, 127);
-        const int q = 4 * i + j - 1;  // the previous pair
+            bf, xa[j], zero, 0, 0, 0, 127, 0, 127);
+        // promote the previous product (one MFMA late, so no FMA waits on
+        // the MFMA it reads)
+        const int q = 2 * i + j - 1;
         if (q >= 0) {
 #pragma unroll
-          for (int r2 = 0; r2 < 4; ++r2) acc[q >> 2][q & 3][r2] += tp[r2] * s_cur[q & 3];
+          for (int r = 0; r < 4; ++r) acc[q >> 1][q & 1][r] += tp[r] * sc[q & 1][(q >> 1) >> 3];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[15][1][r] += tp[r] * s_last;
         }
         tp = t;
       }
-      wf = wf_n;
+      // the step's twelve loads, one per n-tile: weight DMA for step s+3,
+      // then activations and scales for step s+2
+      if (i < 4) dma(cd, dstage, i);
+      else if (i < 12) a_load(L, i - 4, alo[nslot], ahi[nslot], sav[nslot], sbv[nslot]);
+      bf = bn;
+      bn = bnn;
       __builtin_amdgcn_sched_barrier(0);
     }
+    s_last = sc[1][1];
+    if (cc.kb == nk - 1) {
 #pragma unroll
-    for (int r2 = 0; r2 < 4; ++r2) acc[7][3][r2] += tp[r2] * s_cur[3];
+      for (int r = 0; r < 4; ++r) acc[15][1][r] += tp[r] * s_last;
+      tp = zero;
+      s_last = 0.f;
+      epilogue(cc);
+    }
+    advance(cc);
+    advance(ca);
+    advance(cd);
   };
 
-  // One pipeline step: wait for this stage's DMA (and for every wave to leave
-  // the other stage), queue the next block's scales and DMA into the other
-  // stage, then compute this stage.
-  auto step = [&](int kb, const uint8_t* la, const uint8_t* lb, const uint8_t* na,
-                  const uint8_t* nb) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) s_cur[j] = sa_nxt[j] * sb_nxt;
-    if (kb + 1 < nk) {
-      load_scales(kb + 1);
-      const uint32_t k1 = (uint32_t)(kb + 1) * BK;
-      load_tile_lds(ra, offa, k1, na, wave);
-      load_tile_lds(rb, offb, k1, nb, wave);
-    }
-    compute(la, lb);
-  };
-
-  load_scales(0);
-  load_tile_lds(ra, offa, 0, lds, wave);
-  load_tile_lds(rb, offb, 0, lds + TILE_BYTES, wave);
-  for (int kb = 0; kb < nk; ++kb) {
-    const uint8_t* cur = lds + (kb & 1) * 2 * TILE_BYTES;
-    const uint8_t* nxt = lds + ((kb + 1) & 1) * 2 * TILE_BYTES;
-    step(kb, cur, cur + TILE_BYTES, nxt, nxt + TILE_BYTES);
+  const int S = my_tiles * nk;
+  static_assert(PA == 2, "the step loop is unrolled for three activation slots");
+  for (int s = 0; s < S; s += 3) {
+    step(std::integral_constant<int, 0>{}, s);
+    if (s + 1 < S) step(std::integral_constant<int, 1>{}, s + 1);
+    if (s + 2 < S) step(std::integral_constant<int, 2>{}, s + 2);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outlives the workgroup
+}
 
-  // ---- epilogue: lane holds C[m][n .. n+3] for each (i, j) ------------------
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = m0 + 64 * wm + 16 * j + (lane & 15);
-    if (m >= M) continue;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int n = n0 + 128 * wn + 16 * i + 4 * g;
-      // v_cvt_pk_bf16_f32: round-to-nearest-even, as f32_to_bf16
-      const bf16x2 p0 = {(__bf16)acc[i][j][0], (__bf16)acc[i][j][1]};
-      const bf16x2 p1 = {(__bf16)acc[i][j][2], (__bf16)acc[i][j][3]};
-      const uint32_t w0 = __builtin_bit_cast(uint32_t, p0);
-      const uint32_t w1 = __builtin_bit_cast(uint32_t, p1);
-      *reinterpret_cast<uint2*>(C + (long)m * ldc + n) = make_uint2(w0, w1);
-    }
+// Compute units of the current device (one persistent workgroup each).
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
   }
+  return cached[dev];
+}
+
+template <int EPI>
+static int launch_gemm(const GemmArgs& a, qh_stream_t stream, const char* what) {
+  const int tiles = ((a.M + gemm::BM - 1) / gemm::BM) * (a.N / gemm::BR);
+  const int grid = min(tiles, device_cus());
+  hipLaunchKernelGGL(fp8_gemm_kernel<EPI>, dim3(grid), dim3(512), 0, (hipStream_t)stream, a);
+  return launch_status(what);
+}
+
+// Byte ranges the kernel addresses through 32-bit buffer offsets.
+static bool offsets_fit(int M, int N, int K, long lda, long ldb) {
+  const long lim = 0x7fffffffL;
+  return (long)N * ldb < lim && 256L * lda < lim && (long)(K / 128) * M * 4 < lim;
 }
 
 }  // namespace qh
@@ -256,16 +452,34 @@ extern "C" int qh_fp8_gemm_nt(const void* A, long lda, const float* sa, const vo
                               long ldb, const float* sb, void* C, long ldc, int M, int N,
                               int K, qh_stream_t stream) {
   QH_REQUIRE(M >= 0 && N > 0 && K > 0, "fp8_gemm_nt: M=%d N=%d K=%d", M, N, K);
-  QH_REQUIRE(N % gemm::BN == 0, "fp8_gemm_nt: N=%d must be a multiple of 256", N);
+  QH_REQUIRE(N % gemm::BR == 0, "fp8_gemm_nt: N=%d must be a multiple of 256", N);
   QH_REQUIRE(K % gemm::BK == 0, "fp8_gemm_nt: K=%d must be a multiple of 128", K);
   QH_REQUIRE(lda >= K && ldb >= K && ldc >= N, "fp8_gemm_nt: leading dimensions");
   QH_REQUIRE(lda % 16 == 0 && ldb % 16 == 0 && ldc % 4 == 0,
              "fp8_gemm_nt: lda/ldb must be multiples of 16 bytes, ldc of 4 elements");
+  QH_REQUIRE(offsets_fit(M, N, K, lda, ldb), "fp8_gemm_nt: operands exceed 2 GiB offsets");
   if (M == 0) return QH_OK;
   QH_REQUIRE(A && sa && B && sb && C, "fp8_gemm_nt: null pointer");
-  const int tiles = ((M + gemm::BM - 1) / gemm::BM) * (N / gemm::BN);
-  hipLaunchKernelGGL(fp8_gemm_nt_kernel, dim3(tiles), dim3(512), 0,
-                     (hipStream_t)stream, (const uint8_t*)A, lda, sa, (const uint8_t*)B,
-                     ldb, sb, (uint16_t*)C, ldc, M, N, K);
-  return launch_status("fp8_gemm_nt");
+  GemmArgs a{(const uint8_t*)A, lda, sa, (const uint8_t*)B, ldb, sb, C, ldc, nullptr,
+             M, N, K, 0};
+  return launch_gemm<gemm::kStoreBf16>(a, stream, "fp8_gemm_nt");
+}
+
+extern "C" int qh_fp8_gemm_silu_quant(const void* A, long lda, const float* sa,
+                                      const void* B, long ldb, const float* sb, int M,
+                                      int I, int K, void* out_q, long ld_out,
+                                      float* scales, int ue8m0, qh_stream_t stream) {
+  QH_REQUIRE(M >= 0 && I > 0 && K > 0, "fp8_gemm_silu_quant: M=%d I=%d K=%d", M, I, K);
+  QH_REQUIRE(I % 128 == 0, "fp8_gemm_silu_quant: I=%d must be a multiple of 128", I);
+  QH_REQUIRE(K % gemm::BK == 0, "fp8_gemm_silu_quant: K=%d must be a multiple of 128", K);
+  QH_REQUIRE(lda >= K && ldb >= K && ld_out >= I, "fp8_gemm_silu_quant: leading dimensions");
+  QH_REQUIRE(lda % 16 == 0 && ldb % 16 == 0 && ld_out % 4 == 0,
+             "fp8_gemm_silu_quant: lda/ldb must be multiples of 16 bytes, ld_out of 4");
+  QH_REQUIRE(offsets_fit(M, 2 * I, K, lda, ldb),
+             "fp8_gemm_silu_quant: operands exceed 2 GiB offsets");
+  if (M == 0) return QH_OK;
+  QH_REQUIRE(A && sa && B && sb && out_q && scales, "fp8_gemm_silu_quant: null pointer");
+  GemmArgs a{(const uint8_t*)A, lda, sa, (const uint8_t*)B, ldb, sb, out_q, ld_out, scales,
+             M, 2 * I, K, ue8m0};
+  return launch_gemm<gemm::kSiluQuant>(a, stream, "fp8_gemm_silu_quant");
 }

@@ -68,6 +68,16 @@ class Engine:
             return self.gemm_hook(name, q_input.shape[0], w.shape[0], w.shape[1], launch)
         return launch()
 
+    def gemm_silu_quant(self, q_input, input_scale, linear, name="gate_up"):
+        """gate_up GEMM + SiLU gate + fp8 quant in one kernel (gemm then
+        activation_quant, bit-identical)."""
+        w = linear.weight
+        launch = lambda: kernels.fp8_gemm_silu_quant(q_input, input_scale, w,
+                                                     linear.weight_scale, self.use_ue8m0)
+        if self.gemm_hook is not None:
+            return self.gemm_hook(name, q_input.shape[0], w.shape[0], w.shape[1], launch)
+        return launch()
+
     def quant(self, x):
         return kernels.group_quant(x, self.use_ue8m0)
 

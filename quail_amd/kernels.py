@@ -73,12 +73,7 @@ def group_quant(x, ue8m0=False):
     return q, scales
 
 
-def fp8_gemm_nt(a, a_scales, w, w_scales, out=None):
-    """out = (a * a_scales) (w * w_scales)^T in bf16 (DeepGEMM fp8_gemm_nt semantics).
-
-    a [M, K] e4m3 with (M, K/128) column-major fp32 scales; w [N, K] e4m3
-    with (N/128, K/128) fp32 block scales.
-    """
+def _check_gemm(a, a_scales, w, w_scales):
     _check(a, torch.float8_e4m3fn, "a", dim=2)
     _check(w, torch.float8_e4m3fn, "w", dim=2)
     M, K = a.shape
@@ -91,12 +86,41 @@ def fp8_gemm_nt(a, a_scales, w, w_scales, out=None):
     if w_scales.dtype != torch.float32 or tuple(w_scales.shape) != (N // GROUP, K // GROUP) \
             or not w_scales.is_contiguous():
         raise ValueError("w_scales must be contiguous fp32 (N/128, K/128)")
+    return M, N, K
+
+
+def fp8_gemm_nt(a, a_scales, w, w_scales, out=None):
+    """out = (a * a_scales) (w * w_scales)^T in bf16 (DeepGEMM fp8_gemm_nt semantics).
+
+    a [M, K] e4m3 with (M, K/128) column-major fp32 scales; w [N, K] e4m3
+    with (N/128, K/128) fp32 block scales.
+    """
+    M, N, K = _check_gemm(a, a_scales, w, w_scales)
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
     _hip.call("qh_fp8_gemm_nt", _ptr(a), a.stride(0), _ptr(a_scales), _ptr(w),
               w.stride(0), _ptr(w_scales), _ptr(out), out.stride(0), M, N, K,
               _stream())
     return out
+
+
+def fp8_gemm_silu_quant(a, a_scales, w, w_scales, ue8m0=False):
+    """silu_mul_quant(fp8_gemm_nt(a, w)) in one kernel, bit-identical to the pair.
+
+    w is the merged gate_up weight [2I, K] (gate rows, then up rows) with
+    (2I/128, K/128) block scales. Returns the e4m3 [M, I] activation and its
+    (M, I/128) column-major scales (attention.py:300-323 semantics).
+    """
+    M, N, K = _check_gemm(a, a_scales, w, w_scales)
+    if N % (2 * GROUP):
+        raise ValueError(f"gate_up rows {N} must be a multiple of 256")
+    inter = N // 2
+    q = torch.empty((M, inter), dtype=torch.float8_e4m3fn, device=a.device)
+    scales = col_major_scales(M, inter, a.device)
+    _hip.call("qh_fp8_gemm_silu_quant", _ptr(a), a.stride(0), _ptr(a_scales), _ptr(w),
+              w.stride(0), _ptr(w_scales), M, inter, K, _ptr(q), q.stride(0),
+              _ptr(scales), int(bool(ue8m0)), _stream())
+    return q, scales
 
 
 def qk_norm_rope(qkv, positions, cos_sin, q_weight, k_weight, eps, n_q, n_kv,

@@ -4,8 +4,8 @@ ModelPipeline is the contract between the chunk loop and a model family
 (models/base.py:11-47); Qwen3Pipeline is the Qwen3 layer loop
 (models/qwen3.py:46-77): input RMSNorm + fp8 quant, QKV GEMM, per-head Q/K
 RMSNorm + rotary, attention, O GEMM, post-attention RMSNorm + quant (adds
-the residual), gate_up GEMM, SiLU gate + quant, down GEMM; after the last
-layer the answer rows are gathered and final-normed.
+the residual), gate_up GEMM + SiLU gate + quant (one fused kernel), down
+GEMM; after the last layer the answer rows are gathered and final-normed.
 """
 
 from quail_amd import kernels
@@ -79,8 +79,8 @@ class Qwen3Pipeline(ModelPipeline):
             hidden = engine.gemm(o_in, o_scale, attn.o_proj, "o")
             g_in, g_scale = engine.norm_quant(hidden, layer.post_attention_layernorm,
                                               residual)
-            gate_up = engine.gemm(g_in, g_scale, layer.mlp.gate_up_proj, "gate_up")
-            d_in, d_scale = engine.activation_quant(gate_up)
+            # gate_up GEMM + SiLU gate + quant (models/qwen3.py:113-116), fused
+            d_in, d_scale = engine.gemm_silu_quant(g_in, g_scale, layer.mlp.gate_up_proj)
             hidden = engine.gemm(d_in, d_scale, layer.mlp.down_proj, "down")
         if trace is not None:
             trace(len(self.layers), hidden, residual)

@@ -148,6 +148,64 @@ def test_fp8_gemm_nt(M, N, Kd):
     assert (err <= tol).all(), f"max err {err.max().item()} (scale {want.abs().max().item()})"
 
 
+def _gemm_inputs(seed, M, N, Kd, dev):
+    """Random e4m3 activations / weights with random fp32 scales, on `dev`."""
+    g = _gen(seed)
+    a = (torch.randn(M, Kd, generator=g) * 2).to(torch.float8_e4m3fn).to(dev)
+    w = torch.randn(N, Kd, generator=g).to(torch.float8_e4m3fn).to(dev)
+    sa = K.col_major_scales(M, Kd, dev)
+    sa.copy_((torch.rand(M, Kd // 128, generator=g) * 0.02 + 1e-3).to(dev))
+    sw = (torch.rand(N // 128, Kd // 128, generator=g) * 0.01 + 1e-4).to(dev)
+    return a, sa, w, sw
+
+
+@pytest.mark.parametrize("M,N,Kd", [(4096, 4608, 1024), (2333, 19456, 384)])
+def test_fp8_gemm_nt_many_tiles(M, N, Kd):
+    """More tiles than compute units: each persistent workgroup walks several
+    tiles, with loads running across tile boundaries. Reference: the same
+    dequantized operands in an fp32 torch matmul on the GPU."""
+    a, sa, w, sw = _gemm_inputs(11, M, N, Kd, DEV)
+    got = K.fp8_gemm_nt(a, sa, w, sw).float()
+    a32 = a.float() * sa.repeat_interleave(128, dim=1)
+    w32 = w.float() * sw.repeat_interleave(128, dim=0).repeat_interleave(128, dim=1)
+    want = a32 @ w32.t()
+    err = (got - want).abs()
+    tol = want.abs() * 2 ** -8 + 1e-3 * want.abs().max()
+    assert (err <= tol).all(), f"max err {err.max().item()}"
+
+
+@pytest.mark.parametrize("M,I,Kd", [(1, 128, 128), (300, 1024, 2560), (517, 9728, 256),
+                                    (2048, 9728, 512)])
+@pytest.mark.parametrize("ue8m0", [False, True])
+def test_fp8_gemm_silu_quant_matches_pair(M, I, Kd, ue8m0):
+    """The fused gate_up + SiLU + quant kernel equals fp8_gemm_nt followed by
+    silu_mul_quant bit for bit (values and scales)."""
+    a, sa, w, sw = _gemm_inputs(12 + M, M, 2 * I, Kd, DEV)
+    gate_up = K.fp8_gemm_nt(a, sa, w, sw)
+    q_pair, s_pair = K.silu_mul_quant(gate_up, ue8m0)
+    q, s = K.fp8_gemm_silu_quant(a, sa, w, sw, ue8m0)
+    assert torch.equal(s.cpu(), s_pair.cpu())
+    assert torch.equal(q.view(torch.uint8).cpu(), q_pair.view(torch.uint8).cpu())
+
+
+def test_fp8_gemm_silu_quant_oracle():
+    """Against the oracle: fp64 GEMM rounded to bf16, then oracle silu_mul_quant."""
+    g = _gen(13)
+    M, I, Kd = 77, 256, 640
+    w = torch.randn(2 * I, Kd, generator=g) * 0.05
+    wq, ws = ref.quantize_weight_blocks(w)
+    x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    xq, xs = ref.group_quant(x.float())
+    gate_up = ref.fp8_gemm(xq, xs, wq, ws, out_dtype=torch.float64).to(torch.bfloat16)
+    q_ref, s_ref = ref.silu_mul_quant(gate_up)
+    xs_dev = K.col_major_scales(M, Kd, DEV)
+    xs_dev.copy_(xs)
+    q, s = K.fp8_gemm_silu_quant(xq.to(DEV), xs_dev, wq.to(DEV), ws.to(DEV))
+    # the GEMM's fp32 block sums may round a bf16 input one ulp away from the
+    # fp64 reference's, which moves a few outputs by one e4m3 step
+    _check_quant(q, s, q_ref, s_ref, max_frac_off=2e-2, scale_rtol=1e-2)
+
+
 def _paged_case(seed, n_seqs, prefix, max_suffix, n_q=32, n_kv=8, d=128):
     """Sequences sharing a `prefix`-token node, own suffixes, permuted pages."""
     g = _gen(seed)
