@@ -324,6 +324,289 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Paged attention, DMA-fed (the unified path and tree call B).
+//
+// Same workgroup decomposition as attn_fwd_kernel (32 queries x 4 GQA heads,
+// one wave per head) but with 32-key tiles that reach LDS by DMA
+// (buffer_load ... lds) straight from the arena's 4 KiB page blocks, in a
+// 3-stage ring two tiles ahead, and with about half the registers, so three
+// workgroups share a CU. Per tile each wave issues exactly five vector-memory
+// loads - the page id it needs for tile t+3, then its four 1 KiB DMA pieces
+// of tile t+2 (wave w moves K (w < 2) or V^T (w >= 2) of page w % 2) - so
+// every wait is vmcnt(4).
+//
+// LDS stage: K [32 keys][128 d] with 16-byte chunks XOR-swizzled by
+// (key % 16) ^ (key / 16); V^T [2 pages][128 d][16 slots] with the two
+// 16-byte halves of a d row swapped when (d / 8) is odd. The swizzles are
+// applied by choosing which global chunk each DMA lane fetches.
+//
+// The S^T MFMA row i reads key kperm(i) (bits 2 and 3 swapped), so that in
+// each 16-key P.V step a lane's eight P values are eight consecutive keys -
+// exactly sacc[8t .. 8t+7] - and its V^T fragment is one 16-byte read.
+// Pages past the sequence read zeros (zero-length descriptor); the V slots
+// past kv_end of a partial last page are zeroed in LDS, so P = 0 never meets
+// a NaN.
+
+namespace pattn {
+constexpr int BQ = 32;
+constexpr int BKV = 32;
+constexpr int D = 128;
+constexpr int HPW = 4;
+constexpr int PAGE = 16;
+constexpr int NST = 3;             // LDS stages
+constexpr int HALF = BKV * D * 2;  // 8 KiB: K or V^T of one tile
+constexpr int STAGE = 2 * HALF;
+}  // namespace pattn
+
+__device__ __forceinline__ int kperm(int i) {
+  return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
+}
+__device__ __forceinline__ int kswz(int key) { return (key & 15) ^ (key >> 4); }
+
+typedef int pi32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ pi32x4 attn_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t b = (uint64_t)base;
+  return (pi32x4){(int)(uint32_t)b, (int)(uint32_t)(b >> 32), (int)bytes, 0x00020000};
+}
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
+  using namespace pattn;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int col = lane & 31;
+
+  // ---- sequence and q-tile (heaviest tile of a sequence first) -------------
+  const int b = blockIdx.x;
+  const int total_tiles = p.tile_off[p.n_seqs];
+  if (b >= total_tiles) return;
+  int lo = 0, hi = p.n_seqs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (p.tile_off[mid] <= b) lo = mid; else hi = mid - 1;
+  }
+  const int s = lo;
+  const int q0 = p.cu_q[s];
+  const int count = p.cu_q[s + 1] - q0;
+  const int n_qt = (count + BQ - 1) / BQ;
+  const int i0 = (n_qt - 1 - (b - p.tile_off[s])) * BQ;
+  const int kv_len = p.kv_len[s];
+  const int group = p.n_q / p.n_kv;
+  const int hq = blockIdx.y * HPW + wave;
+  const int hk = (blockIdx.y * HPW) / group;
+  int kv_end = kv_len;
+  if (CAUSAL) kv_end = min(kv_len, kv_len - count + min(i0 + BQ, count));
+  kv_end = max(kv_end, 0);
+  const int n_tiles = (kv_end + BKV - 1) / BKV;
+  const int my_i = i0 + col;
+  const int lim = CAUSAL ? min(kv_len, kv_len - count + my_i + 1) : kv_len;
+
+  // ---- DMA roles ------------------------------------------------------------
+  const int region = wave >> 1;  // 0: K, 1: V^T
+  const int pit = wave & 1;      // page within the tile
+  uint32_t voff[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int P = 1024 * c + 16 * lane;  // byte position in the LDS page block
+    if (region == 0) {
+      const int r16 = P >> 8, pc = (P >> 4) & 15;
+      voff[c] = (uint32_t)(r16 * 256 + ((pc ^ kswz(16 * pit + r16)) * 16));
+    } else {
+      const int d = P >> 5, ph = (P >> 4) & 1;
+      voff[c] = (uint32_t)(d * 32 + ((ph ^ ((d >> 3) & 1)) * 16));
+    }
+  }
+  const uint16_t* pool = region ? p.v_pool : p.k_pool;
+  const pi32x4 rtab = attn_rsrc(p.table, (uint32_t)p.n_seqs * (uint32_t)p.table_width * 4u);
+  const long tab_row = (long)s * p.table_width;
+  // page index of this wave's page in tile t, clamped into the table row
+  auto tab_off = [&](int t) __attribute__((always_inline)) {
+    const int pidx = min(2 * t + pit, p.table_width - 1);
+    return (uint32_t)((tab_row + pidx) * 4);
+  };
+  auto load_page_id = [&](int t, float& dst) __attribute__((always_inline)) {
+    asm volatile("buffer_load_dword %0, off, %1, %2"
+                 : "=v"(dst) : "s"(rtab), "s"(tab_off(t)) : "memory");
+  };
+  // this wave's four DMA pieces of tile t into stage t % NST
+  auto dma_tile = [&](int t, int page_id) __attribute__((always_inline)) {
+    const int pidx = 2 * t + pit;
+    const bool live = t < n_tiles && pidx < p.table_width && pidx * PAGE < kv_end &&
+                      page_id >= 0 && page_id < p.pool_pages;
+    const int slots = live ? min(PAGE, kv_end - pidx * PAGE) : 0;
+    const uint32_t bytes = region ? (live ? 4096u : 0u) : (uint32_t)slots * 256u;
+    const uint16_t* blk = pool + ((long)(live ? page_id : 0) * p.n_kv + hk) * (PAGE * D);
+    const pi32x4 rs = attn_rsrc(blk, bytes);
+    const uint32_t base =
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(
+            lds + (t % NST) * STAGE + region * HALF + pit * 4096);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      asm volatile(
+          "s_mov_b32 m0, %0\n\t"
+          "buffer_load_dwordx4 %1, %2, 0 offen lds"
+          :
+          : "s"(base + 1024 * c), "v"(voff[c]), "s"(rs)
+          : "memory", "m0");
+  };
+
+  // ---- Q fragments: lane holds Q[query col][16*st + 8*half .. +7] -----------
+  typedef int qi32x4 __attribute__((ext_vector_type(4)));
+  qi32x4 qraw[8];
+  {
+    long row = q0 + my_i;
+    bool ok = my_i < count;
+    if (ok && p.q_rows) row = p.q_rows[row];
+    ok = ok && row >= 0 && row < p.q_rows_total;
+    const uint32_t qoff = ok ? (uint32_t)(row * p.ldq * 2 + (long)hq * D * 2 + 16 * half)
+                             : 0x80000000u;
+    const pi32x4 rq = attn_rsrc(p.q, (uint32_t)((long)p.q_rows_total * p.ldq * 2));
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+      asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3"
+                   : "=v"(qraw[st]) : "v"(qoff), "s"(rq), "i"(32 * st) : "memory");
+  }
+
+  // ---- prologue: page ids of tiles 0..2 (scalar), DMA of tiles 0 and 1 -------
+  int pg0 = -1, pg1 = -1, pg2 = -1;
+  if (n_tiles > 0) {
+    pg0 = p.table[tab_row + min(pit, p.table_width - 1)];
+    pg1 = p.table[tab_row + min(2 + pit, p.table_width - 1)];
+    pg2 = p.table[tab_row + min(4 + pit, p.table_width - 1)];
+    dma_tile(0, pg0);
+    dma_tile(1, pg1);
+  }
+  asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // Q and tile 0 landed
+  asm volatile("" : "+v"(qraw[0]), "+v"(qraw[1]), "+v"(qraw[2]), "+v"(qraw[3]),
+               "+v"(qraw[4]), "+v"(qraw[5]), "+v"(qraw[6]), "+v"(qraw[7]));
+  bf16x8_t qf[8];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) qf[st] = __builtin_bit_cast(bf16x8_t, qraw[st]);
+
+  f32x16 acc_o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int a = 0; a < 16; ++a) acc_o[db][a] = 0.f;
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  float pg_next = __builtin_bit_cast(float, pg2);  // page id for the DMA of tile t+2
+
+  const int kq = kperm(col);  // key row this lane's S^T row reads
+  for (int t = 0; t < n_tiles; ++t) {
+    // tile t's DMA (issued two tiles back) and the page id of tile t+2
+    // (issued first last tile) have landed; tile t+1's DMA may be in flight
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    asm volatile("" : "+v"(pg_next));
+    const int page_t2 = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, pg_next));
+    __syncthreads();  // stage t visible to all; stage t-1 free
+    load_page_id(t + 3, pg_next);
+    dma_tile(t + 2, page_t2);
+
+    uint8_t* st_base = lds + (t % NST) * STAGE;
+    const int key0 = t * BKV;
+    // a partial last page: zero its V^T slots past kv_end
+    if (key0 + BKV > kv_end && ((kv_end & (PAGE - 1)) != 0)) {
+      const int zpit = (kv_end - key0) >> 4;
+      const int valid = kv_end & (PAGE - 1);
+      if (zpit < 2) {
+        const int d = tid >> 1, ph = tid & 1;
+        const int lh = ph ^ ((d >> 3) & 1);
+        uint16_t* vp = reinterpret_cast<uint16_t*>(st_base + HALF + zpit * 4096 + d * 32 + ph * 16);
+        bf16x8 v = load8(vp);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (8 * lh + e >= valid) v.set(e, 0);
+        store8(vp, v);
+      }
+      __syncthreads();
+    }
+
+    // ---- S^T = K Q^T ---------------------------------------------------------
+    f32x16 sacc;
+#pragma unroll
+    for (int a = 0; a < 16; ++a) sacc[a] = 0.f;
+    const uint8_t* krow = st_base + kq * 256;
+    const int ksw = kswz(kq);
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const bf16x8_t af =
+          *reinterpret_cast<const bf16x8_t*>(krow + (((2 * st + half) ^ ksw) * 16));
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[st], sacc, 0, 0, 0);
+    }
+    // ---- mask, scale, online softmax (log2 domain) -------------------------
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int a = 0; a < 16; ++a) {
+      const int key = key0 + kperm(8 * (a >> 2) + 4 * half + (a & 3));
+      const float v = key < lim ? sacc[a] * p.scale_log2 : -INFINITY;
+      sacc[a] = v;
+      tmax = fmaxf(tmax, v);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+    float psum = 0.f;
+#pragma unroll
+    for (int a = 0; a < 16; ++a) {
+      const float e = (m_new == -INFINITY) ? 0.f : exp2f(sacc[a] - m_new);
+      sacc[a] = e;
+      psum += e;
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int a = 0; a < 16; ++a) acc_o[db][a] *= alpha;
+
+    // ---- O^T += V^T P^T over the tile's two pages ----------------------------
+#pragma unroll
+    for (int pt = 0; pt < 2; ++pt) {
+      bf16x8_t pf;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pf[e] = (__bf16)sacc[8 * pt + e];
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int d = 32 * db + col;
+        const bf16x8_t vf = *reinterpret_cast<const bf16x8_t*>(
+            st_base + HALF + pt * 4096 + d * 32 + ((half ^ ((d >> 3) & 1)) * 16));
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc_o[db], 0, 0, 0);
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outlives the workgroup
+
+  // ---- epilogue -------------------------------------------------------------
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (my_i >= count) return;
+  const long qi = q0 + my_i;
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  uint16_t* op = p.out + qi * p.ldo + (long)hq * D;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d = 32 * db + 8 * g + 4 * half;
+      uint32_t w0 = f32_to_bf16(acc_o[db][4 * g + 0] * inv) |
+                    (f32_to_bf16(acc_o[db][4 * g + 1] * inv) << 16);
+      uint32_t w1 = f32_to_bf16(acc_o[db][4 * g + 2] * inv) |
+                    (f32_to_bf16(acc_o[db][4 * g + 3] * inv) << 16);
+      *reinterpret_cast<uint2*>(op + d) = make_uint2(w0, w1);
+    }
+  if (p.lse && half == 0) {
+    const float lse = l_tot > 0.f ? (m_run + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+    p.lse[(long)hq * p.lse_stride + qi] = lse;
+  }
+}
+
 }  // namespace qh
 
 using namespace qh;
@@ -353,6 +636,10 @@ extern "C" int qh_attention(const void* q, long ldq, int q_rows_total, const int
   if (paged) {
     QH_REQUIRE(k_pool && v_pool && pool_pages > 0 && table_width > 0,
                "attention: paged call without pools/table");
+    // the paged kernel addresses q and the table through 32-bit buffer offsets
+    QH_REQUIRE((long)q_rows_total * ldq * 2 < 0x80000000L &&
+                   (long)n_seqs * table_width * 4 < 0x80000000L,
+               "attention: q (%d rows) or page table exceeds 2 GiB", q_rows_total);
     QH_REQUIRE(page_tokens == attn::PAGE, "attention: page_tokens %d unsupported (16 only)",
                page_tokens);
   } else {
@@ -397,8 +684,8 @@ extern "C" int qh_attention(const void* q, long ldq, int q_rows_total, const int
   const long max_tiles = (long)n_queries / attn::BQ + n_seqs;
   dim3 grid((unsigned)max_tiles, (unsigned)(n_q / attn::HPW));
   if (paged) {
-    if (causal) hipLaunchKernelGGL((attn_fwd_kernel<true, true>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((attn_fwd_kernel<true, false>), grid, dim3(256), 0, st, p);
+    if (causal) hipLaunchKernelGGL((attn_paged_kernel<true>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((attn_paged_kernel<false>), grid, dim3(256), 0, st, p);
   } else {
     if (causal) hipLaunchKernelGGL((attn_fwd_kernel<false, true>), grid, dim3(256), 0, st, p);
     else hipLaunchKernelGGL((attn_fwd_kernel<false, false>), grid, dim3(256), 0, st, p);
