@@ -62,9 +62,11 @@ class KernelClock:
         e1.record()
         flops = 4.0 * self.n_q * self.d * pairs
         # unified gather: each sequence reads its own K and V rows (the node is
-        # re-read per sequence), plus Q in and O out
+        # re-read per sequence), plus Q in (bf16) and O out (e4m3 for the
+        # unified call, which quantizes in its epilogue; bf16 otherwise)
+        out_bytes = 1 if kind == "unified" else 2
         nbytes = (kv_rows * self.n_kv * self.d * 2 * 2
-                  + 2 * n_queries * self.n_q * self.d * 2)
+                  + n_queries * self.n_q * self.d * (2 + out_bytes))
         self.attn.append((flops, nbytes, e0, e1, kind))
         return out
 

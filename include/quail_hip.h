@@ -182,6 +182,25 @@ int qh_attention(const void* q, long ldq, int q_rows_total,
                  size_t workspace_bytes, qh_stream_t stream);
 
 /*
+ * The unified path's paged causal call fused with the fp8 quantization that
+ * follows it: replaces Engine.attention's _paged + quant (attention.py:939-943
+ * then :798). Same inputs as the paged form of qh_attention; instead of bf16
+ * out it writes out_q [n_queries, n_q*128] e4m3 (row stride ld_out_q bytes)
+ * and scales [n_q, n_queries] fp32, one 1x128 group per (row, head), computed
+ * from the bf16-rounded output exactly as qh_group_quant would: bit-identical
+ * to qh_attention followed by qh_group_quant.
+ */
+int qh_attention_fp8(const void* q, long ldq, int q_rows_total,
+                     const int64_t* q_rows, const void* k_pool,
+                     const void* v_pool, int pool_pages, const int32_t* table,
+                     int table_width, int page_tokens, const int32_t* cu_q,
+                     const int32_t* kv_len, int n_seqs, int n_queries, int max_q,
+                     int n_q, int n_kv, int d, float softmax_scale, int causal,
+                     void* out_q, long ld_out_q, float* scales, int ue8m0,
+                     void* workspace, size_t workspace_bytes,
+                     qh_stream_t stream);
+
+/*
  * LSE merge of the tree path's two attention calls fused with per-head fp8
  * quantization. Replaces Triton merge_attn_quant (attention.py:429-473,
  * :738-759): where source[t] >= 0, w = bf16(sigmoid(lse_b - lse_a)),

@@ -55,6 +55,13 @@ struct AttnParams {
   float* lse;
   long lse_stride;
   const int32_t* tile_off;  // [n_seqs + 1] exclusive scan of q-tiles
+  // fp8 output (attn_paged_kernel with FP8OUT): e4m3 [n_out, n_q*128] and
+  // per-(row, head) scales [n_q, n_out]
+  uint8_t* out_q;
+  long ld_out_q;
+  float* out_scales;
+  int n_out;
+  int ue8m0;
 };
 
 // Exclusive scan of per-sequence q-tile counts into tile_off[0..n_seqs].
@@ -372,7 +379,7 @@ __device__ __forceinline__ pi32x4 attn_rsrc(const void* base, uint32_t bytes) {
   return (pi32x4){(int)(uint32_t)b, (int)(uint32_t)(b >> 32), (int)bytes, 0x00020000};
 }
 
-template <bool CAUSAL>
+template <bool CAUSAL, bool FP8OUT>
 __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
   using namespace pattn;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
@@ -586,21 +593,50 @@ __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
 
   // ---- epilogue -------------------------------------------------------------
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  if (my_i >= count) return;
-  const long qi = q0 + my_i;
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  uint16_t* op = p.out + qi * p.ldo + (long)hq * D;
+  const long qi = q0 + my_i;
+  if constexpr (FP8OUT) {
+    // the bf16 output, quantized per (row, head) 128-wide group exactly as
+    // group_quant would quantize it; the group's other 64 values sit in the
+    // partner lane (lane ^ 32)
+    float amax = 0.f;
 #pragma unroll
-  for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = 32 * db + 8 * g + 4 * half;
-      uint32_t w0 = f32_to_bf16(acc_o[db][4 * g + 0] * inv) |
-                    (f32_to_bf16(acc_o[db][4 * g + 1] * inv) << 16);
-      uint32_t w1 = f32_to_bf16(acc_o[db][4 * g + 2] * inv) |
-                    (f32_to_bf16(acc_o[db][4 * g + 3] * inv) << 16);
-      *reinterpret_cast<uint2*>(op + d) = make_uint2(w0, w1);
-    }
+      for (int a = 0; a < 16; ++a) {
+        const float v = round_bf16(acc_o[db][a] * inv);
+        acc_o[db][a] = v;
+        amax = fmaxf(amax, fabsf(v));
+      }
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    if (my_i >= count) return;
+    const float scale = group_scale(amax, p.ue8m0 != 0);
+    uint8_t* qp = p.out_q + qi * p.ld_out_q + (long)hq * D;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w |= quant_e4m3(acc_o[db][4 * g + r], scale) << (8 * r);
+        *reinterpret_cast<uint32_t*>(qp + 32 * db + 8 * g + 4 * half) = w;
+      }
+    if (half == 0) p.out_scales[(long)hq * p.n_out + qi] = scale;
+  } else {
+    if (my_i >= count) return;
+    uint16_t* op = p.out + qi * p.ldo + (long)hq * D;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * db + 8 * g + 4 * half;
+        uint32_t w0 = f32_to_bf16(acc_o[db][4 * g + 0] * inv) |
+                      (f32_to_bf16(acc_o[db][4 * g + 1] * inv) << 16);
+        uint32_t w1 = f32_to_bf16(acc_o[db][4 * g + 2] * inv) |
+                      (f32_to_bf16(acc_o[db][4 * g + 3] * inv) << 16);
+        *reinterpret_cast<uint2*>(op + d) = make_uint2(w0, w1);
+      }
+  }
   if (p.lse && half == 0) {
     const float lse = l_tot > 0.f ? (m_run + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
     p.lse[(long)hq * p.lse_stride + qi] = lse;
@@ -615,23 +651,31 @@ extern "C" size_t qh_attention_workspace_bytes(int n_seqs) {
   return (size_t)(n_seqs + 1) * sizeof(int32_t) + 256;
 }
 
-extern "C" int qh_attention(const void* q, long ldq, int q_rows_total, const int64_t* q_rows,
+// Shared by qh_attention and qh_attention_fp8: checks, tile scan, launch.
+static int attention_launch(const void* q, long ldq, int q_rows_total, const int64_t* q_rows,
                             const void* k_pool, const void* v_pool, int pool_pages,
                             const int32_t* table, int table_width, int page_tokens,
                             const void* k_rows, const void* v_rows, int kv_rows_total,
                             const int32_t* cu_k, const int32_t* cu_q, const int32_t* kv_len,
                             int n_seqs, int n_queries, int max_q, int n_q, int n_kv, int d,
                             float softmax_scale, int causal, void* out, long ldo, float* lse,
-                            long lse_stride, void* workspace, size_t workspace_bytes,
+                            long lse_stride, void* out_q, long ld_out_q, float* out_scales,
+                            int ue8m0, void* workspace, size_t workspace_bytes,
                             qh_stream_t stream) {
   QH_REQUIRE(d == attn::D, "attention: head_dim %d unsupported (128 only)", d);
   QH_REQUIRE(n_q > 0 && n_kv > 0 && n_q % n_kv == 0 && (n_q / n_kv) % attn::HPW == 0,
              "attention: n_q=%d n_kv=%d needs a GQA group that is a multiple of 4", n_q, n_kv);
   QH_REQUIRE(n_seqs >= 0 && n_queries >= 0 && max_q >= 0, "attention: negative sizes");
   if (n_seqs == 0 || n_queries == 0) return QH_OK;
-  QH_REQUIRE(q && cu_q && kv_len && out, "attention: null pointer");
-  QH_REQUIRE(ldq >= (long)n_q * d && ldq % 8 == 0 && ldo >= (long)n_q * d && ldo % 8 == 0,
-             "attention: row strides ldq=%ld ldo=%ld", ldq, ldo);
+  const bool fp8 = out_q != nullptr;
+  QH_REQUIRE(q && cu_q && kv_len && (fp8 ? out_scales != nullptr : out != nullptr),
+             "attention: null pointer");
+  QH_REQUIRE(ldq >= (long)n_q * d && ldq % 8 == 0, "attention: row stride ldq=%ld", ldq);
+  if (fp8)
+    QH_REQUIRE(ld_out_q >= (long)n_q * d && ld_out_q % 16 == 0,
+               "attention: fp8 row stride %ld", ld_out_q);
+  else
+    QH_REQUIRE(ldo >= (long)n_q * d && ldo % 8 == 0, "attention: row stride ldo=%ld", ldo);
   const bool paged = table != nullptr;
   if (paged) {
     QH_REQUIRE(k_pool && v_pool && pool_pages > 0 && table_width > 0,
@@ -643,6 +687,7 @@ extern "C" int qh_attention(const void* q, long ldq, int q_rows_total, const int
     QH_REQUIRE(page_tokens == attn::PAGE, "attention: page_tokens %d unsupported (16 only)",
                page_tokens);
   } else {
+    QH_REQUIRE(!fp8, "attention: fp8 output needs the paged path");
     QH_REQUIRE(k_rows && v_rows && cu_k && kv_rows_total > 0,
                "attention: contiguous call without k_rows/v_rows/cu_k");
   }
@@ -680,15 +725,57 @@ extern "C" int qh_attention(const void* q, long ldq, int q_rows_total, const int
   p.lse = lse;
   p.lse_stride = lse_stride;
   p.tile_off = tile_off;
+  p.out_q = (uint8_t*)out_q;
+  p.ld_out_q = ld_out_q;
+  p.out_scales = out_scales;
+  p.n_out = n_queries;
+  p.ue8m0 = ue8m0;
   // upper bound on the q-tiles: sum ceil(c/32) <= n_queries/32 + n_seqs
   const long max_tiles = (long)n_queries / attn::BQ + n_seqs;
   dim3 grid((unsigned)max_tiles, (unsigned)(n_q / attn::HPW));
   if (paged) {
-    if (causal) hipLaunchKernelGGL((attn_paged_kernel<true>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((attn_paged_kernel<false>), grid, dim3(256), 0, st, p);
+    if (fp8) {
+      if (causal) hipLaunchKernelGGL((attn_paged_kernel<true, true>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((attn_paged_kernel<false, true>), grid, dim3(256), 0, st, p);
+    } else {
+      if (causal) hipLaunchKernelGGL((attn_paged_kernel<true, false>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((attn_paged_kernel<false, false>), grid, dim3(256), 0, st, p);
+    }
   } else {
     if (causal) hipLaunchKernelGGL((attn_fwd_kernel<false, true>), grid, dim3(256), 0, st, p);
     else hipLaunchKernelGGL((attn_fwd_kernel<false, false>), grid, dim3(256), 0, st, p);
   }
   return launch_status("attention");
+}
+
+extern "C" int qh_attention(const void* q, long ldq, int q_rows_total, const int64_t* q_rows,
+                            const void* k_pool, const void* v_pool, int pool_pages,
+                            const int32_t* table, int table_width, int page_tokens,
+                            const void* k_rows, const void* v_rows, int kv_rows_total,
+                            const int32_t* cu_k, const int32_t* cu_q, const int32_t* kv_len,
+                            int n_seqs, int n_queries, int max_q, int n_q, int n_kv, int d,
+                            float softmax_scale, int causal, void* out, long ldo, float* lse,
+                            long lse_stride, void* workspace, size_t workspace_bytes,
+                            qh_stream_t stream) {
+  return attention_launch(q, ldq, q_rows_total, q_rows, k_pool, v_pool, pool_pages, table,
+                          table_width, page_tokens, k_rows, v_rows, kv_rows_total, cu_k, cu_q,
+                          kv_len, n_seqs, n_queries, max_q, n_q, n_kv, d, softmax_scale, causal,
+                          out, ldo, lse, lse_stride, nullptr, 0, nullptr, 0, workspace,
+                          workspace_bytes, stream);
+}
+
+extern "C" int qh_attention_fp8(const void* q, long ldq, int q_rows_total,
+                                const int64_t* q_rows, const void* k_pool, const void* v_pool,
+                                int pool_pages, const int32_t* table, int table_width,
+                                int page_tokens, const int32_t* cu_q, const int32_t* kv_len,
+                                int n_seqs, int n_queries, int max_q, int n_q, int n_kv, int d,
+                                float softmax_scale, int causal, void* out_q, long ld_out_q,
+                                float* scales, int ue8m0, void* workspace,
+                                size_t workspace_bytes, qh_stream_t stream) {
+  QH_REQUIRE(table && out_q && scales, "attention_fp8: paged call needs table, out_q, scales");
+  return attention_launch(q, ldq, q_rows_total, q_rows, k_pool, v_pool, pool_pages, table,
+                          table_width, page_tokens, nullptr, nullptr, 0, nullptr, cu_q, kv_len,
+                          n_seqs, n_queries, max_q, n_q, n_kv, d, softmax_scale, causal,
+                          nullptr, 0, nullptr, 0, out_q, ld_out_q, scales, ue8m0, workspace,
+                          workspace_bytes, stream);
 }

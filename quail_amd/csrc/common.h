@@ -83,6 +83,18 @@ __device__ __forceinline__ uint32_t quant_e4m3(float y, float scale) {
   return f32_to_e4m3(q);
 }
 
+// silu(g) * u = g * sigmoid(g) * u in fp32 with sigmoid(g) = 1 / (1 + e^-g)
+// from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32): the same
+// formula the reference's Triton kernel evaluates with its fast exp and
+// division (attention.py:311). Products are not contracted, so every caller
+// gets the same bits.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+  const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+  const float sig = __builtin_amdgcn_rcpf(1.0f + e);
+  return g * sig * u;
+}
+
 // ---- lane reductions (wave64) -----------------------------------------------
 
 template <int WIDTH>

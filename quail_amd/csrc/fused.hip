@@ -127,9 +127,7 @@ __global__ __launch_bounds__(256) void silu_mul_quant_kernel(
   float amax = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float gate = gv.get(e);
-    const float sig = 1.0f / (1.0f + expf(-gate));
-    y[e] = gate * sig * uv.get(e);
+    y[e] = silu_mul(gv.get(e), uv.get(e));
     amax = fmaxf(amax, fabsf(y[e]));
   }
   amax = group_max<16>(amax);

@@ -84,11 +84,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // silu(gate) * up of one GEMM output pair, with both rounded to bf16 first:
 // the same arithmetic as silu_mul_quant_kernel on a bf16 gate_up tensor.
 __device__ __forceinline__ float silu_mul_bf16(float gate_acc, float up_acc) {
-#pragma clang fp contract(off)
-  const float gate = round_bf16(gate_acc);
-  const float up = round_bf16(up_acc);
-  const float sig = 1.0f / (1.0f + expf(-gate));
-  return gate * sig * up;
+  return silu_mul(round_bf16(gate_acc), round_bf16(up_acc));
 }
 
 template <int EPI>

@@ -116,7 +116,7 @@ class Engine:
         v3 = v.contiguous().view(n, KH, D)
         if chunk.attention_mode == "tree":
             return self.attention_tree(q3, k3, v3, chunk.meta, n)
-        return self.quant(self.attention_unified(q3, k3, v3, chunk.meta, n))
+        return self.attention_unified(q3, k3, v3, chunk.meta, n)
 
     def _timed(self, kind, pairs, kv_rows, n_queries, launch):
         if self.attention_hook is None:
@@ -133,25 +133,28 @@ class Engine:
             cu_k=meta["cu_a"], n_kv=self.num_kv_heads, want_lse=want_lse))
 
     def attention_unified(self, q3, k3, v3, meta, n):
+        """Unified path; returns the quantized o_proj input (e4m3, scales)."""
         layer = meta["layer"]
         unified = meta["unified"]
         if unified is None:
             out, _ = self._causal_own(q3, k3, v3, meta, n, want_lse=False)
             meta["layer"] += 1
-            return out.view(n, -1)
+            return self.quant(out.view(n, -1))
         k_pool, v_pool = self.arena.layer_kv(layer)
         kernels.kv_row_scatter(k3, v3, k_pool, v_pool, unified["src"], unified["dst"])
         if unified["tail_src"] is not None:
             kernels.kv_row_copy(k_pool, v_pool, unified["tail_src"], unified["tail_dst"])
         work = meta.get("work", {})
-        out, _ = self._timed(
+        # the paged causal call with the per-head fp8 quant in its epilogue
+        q_out = self._timed(
             "unified", work.get("unified_pairs", 0), work.get("unified_kv_rows", 0), n,
-            lambda: kernels.attention(
+            lambda: kernels.attention_fp8(
                 q3, unified["cu_q"], unified["used"], n_queries=n, max_q=unified["max_q"],
                 softmax_scale=self.softmax_scale, causal=True, k_pool=k_pool,
-                v_pool=v_pool, table=unified["table"], n_kv=self.num_kv_heads))
+                v_pool=v_pool, table=unified["table"], n_kv=self.num_kv_heads,
+                ue8m0=self.use_ue8m0))
         meta["layer"] += 1
-        return out.view(n, -1)
+        return q_out
 
     def attention_tree(self, q3, k3, v3, meta, n):
         layer = meta["layer"]

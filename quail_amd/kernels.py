@@ -205,6 +205,28 @@ def attention(q3, cu_q, kv_len, *, n_queries, max_q, softmax_scale, causal,
     return out, lse
 
 
+def attention_fp8(q3, cu_q, kv_len, *, n_queries, max_q, softmax_scale, causal,
+                  k_pool, v_pool, table, n_kv, q_rows=None, ue8m0=False):
+    """Paged attention whose output is fp8-quantized per (row, head) in the
+    kernel: (e4m3 [n_queries, n_q*d], scales (n_queries, n_q) column-major),
+    bit-identical to group_quant(attention(...)) (attention.py:939-943, :798)."""
+    _check(q3, torch.bfloat16, "q", dim=3)
+    rows, n_q, d = q3.shape
+    if d != GROUP:
+        raise ValueError("one quant group per head needs head_dim 128")
+    n_seqs = cu_q.numel() - 1
+    dev = q3.device
+    q = torch.empty((n_queries, n_q * d), dtype=torch.float8_e4m3fn, device=dev)
+    scales = col_major_scales(n_queries, n_q * d, dev)
+    ws = torch.empty(_hip.workspace_bytes(n_seqs), dtype=torch.uint8, device=dev)
+    _hip.call("qh_attention_fp8", _ptr(q3), q3.stride(0), rows, _ptr(q_rows),
+              _ptr(k_pool), _ptr(v_pool), k_pool.shape[0], _ptr(table), table.shape[1],
+              PAGE_TOKENS, _ptr(cu_q), _ptr(kv_len), n_seqs, int(n_queries), int(max_q),
+              n_q, n_kv, d, float(softmax_scale), int(bool(causal)), _ptr(q), q.stride(0),
+              _ptr(scales), int(bool(ue8m0)), _ptr(ws), ws.numel(), _stream())
+    return q, scales
+
+
 def merge_attn_quant(out_a, lse_a, out_b, lse_b, source, ue8m0=False):
     """LSE merge of the tree path + per-head fp8 quant (attention.py:429-473).
 

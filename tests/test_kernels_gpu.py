@@ -267,6 +267,51 @@ def test_paged_attention_causal(seed, n_seqs, prefix, max_suffix):
     assert torch.allclose(lse, want_lse, atol=2e-3, rtol=0)
 
 
+def test_paged_attention_ignores_unread_rows():
+    """Arena rows no sequence reads (past `used` in a last page, whole unused
+    pages) hold NaN: the kernel must not let them into any output."""
+    case = _paged_case(14, 7, 48, 90)
+    page = 16
+    read = torch.zeros(case["k_rows"].shape[0], dtype=torch.bool)
+    for s in range(case["table"].shape[0]):
+        for j in range(int(case["used"][s])):
+            read[int(case["table"][s, j // page]) * page + j % page] = True
+    nan_case = dict(case, k_rows=case["k_rows"].clone(), v_rows=case["v_rows"].clone())
+    nan_case["k_rows"][~read] = float("nan")
+    nan_case["v_rows"][~read] = float("nan")
+    got, lse, want, want_lse = _run_paged(nan_case, causal=True)
+    assert torch.isfinite(got).all() and torch.isfinite(lse).all()
+    assert (got - want).abs().max().item() <= 2e-3
+    assert torch.allclose(lse, want_lse, atol=2e-3, rtol=0)
+
+
+@pytest.mark.parametrize("causal,gathered", [(True, False), (False, True)])
+@pytest.mark.parametrize("ue8m0", [False, True])
+def test_attention_fp8_matches_quantized_bf16(causal, gathered, ue8m0):
+    """The fp8-output attention equals attention (bf16) then group_quant,
+    bit for bit."""
+    case = _paged_case(40 + int(causal), 9, 80, 120)
+    T = int(case["cu_q"][-1])
+    q3, rows = case["q"], None
+    if gathered:
+        g = _gen(41)
+        big = torch.randn(T + 30, 32, 128, generator=g).to(torch.bfloat16)
+        rows = torch.randperm(T + 30, generator=g)[:T].sort().values
+        big[rows] = case["q"]
+        q3, rows = big, rows.to(DEV)
+    kp = layout.k_pool_from_rows(case["k_rows"]).to(DEV)
+    vp = layout.v_pool_from_rows(case["v_rows"]).to(DEV)
+    args = dict(n_queries=T, max_q=case["max_q"], softmax_scale=1 / math.sqrt(128),
+                causal=causal, k_pool=kp, v_pool=vp, table=case["table"].to(DEV),
+                q_rows=rows, n_kv=case["n_kv"])
+    out, _ = K.attention(q3.to(DEV), case["cu_q"].to(DEV), case["used"].to(DEV), **args)
+    q_ref, s_ref = K.group_quant(out.view(T, -1), ue8m0)
+    q, s = K.attention_fp8(q3.to(DEV), case["cu_q"].to(DEV), case["used"].to(DEV),
+                           ue8m0=ue8m0, **args)
+    assert torch.equal(s.cpu(), s_ref.cpu())
+    assert torch.equal(q.view(torch.uint8).cpu(), q_ref.view(torch.uint8).cpu())
+
+
 def test_paged_attention_noncausal_gathered_rows():
     case = _paged_case(20, 6, 128, 60)
     T = int(case["cu_q"][-1])
