@@ -209,26 +209,51 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 // KV append into the paged arena. K pages hold [n_kv][page][d]; V pages hold
 // [n_kv][d][page]. One wave per row pair; K moves as 16-byte vectors, V as
 // 2-byte elements into its transposed page column.
+// Chunk rows -> arena rows for the layer's K and V pools (attention.py:411-427
+// semantics; the arena layout is the one in quail_hip.h). One workgroup moves
+// 16 consecutive entries. K rows are copied as 16-byte chunks. V rows are
+// staged in LDS and written as V^T with the entry index fastest across lanes:
+// entries that land in consecutive slots of one page give one contiguous
+// 32-byte write per (page, head, d) row, wherever the run starts or breaks.
+constexpr int kScatterRows = 16;
+
 __global__ __launch_bounds__(256) void kv_scatter_kernel(
     const uint16_t* __restrict__ k_src, const uint16_t* __restrict__ v_src,
     uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
     const int64_t* __restrict__ src, const int64_t* __restrict__ dst, int n,
     int n_kv, int page) {
-  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (i >= n) return;
-  const int lane = threadIdx.x & 63;
-  const long s = src[i], r = dst[i];
-  const long pg = r / page, slot = r % page;
-  const int row_vecs = n_kv * 16;  // 8-element vectors per row
-  for (int c = lane; c < row_vecs; c += 64) {
-    const int h = c >> 4, off = (c & 15) * 8;
-    bf16x8 kv = load8(k_src + (s * n_kv + h) * 128 + off);
-    store8(k_pool + ((pg * n_kv + h) * page + slot) * 128 + off, kv);
-    bf16x8 vv = load8(v_src + (s * n_kv + h) * 128 + off);
-    uint16_t* vb = v_pool + ((pg * n_kv + h) * 128 + off) * page + slot;
+  // V rows of the 16 entries, [entry][n_kv*128] with a 4-byte pad per entry
+  // so the transposed reads (entry fastest) fall in distinct banks
+  extern __shared__ uint16_t vbuf[];
+  const int row_elems = n_kv * 128;
+  const int ld = row_elems + 2;
+  const int tid = threadIdx.x;
+  const int i0 = blockIdx.x * kScatterRows;
+  const int rows = min(kScatterRows, n - i0);
+  const int chunks = rows * n_kv * 16;  // 16-byte chunks of K (and of V)
+  for (int c = tid; c < chunks; c += 256) {
+    const int e = c / (n_kv * 16), hc = c % (n_kv * 16);
+    const int h = hc >> 4, off = (hc & 15) * 8;
+    const long s = src[i0 + e], r = dst[i0 + e];
+    const long pg = r / page, slot = r % page;
+    store8(k_pool + ((pg * n_kv + h) * page + slot) * 128 + off,
+           load8(k_src + (s * n_kv + h) * 128 + off));
+    const bf16x8 vv = load8(v_src + (s * n_kv + h) * 128 + off);
+    uint32_t* vl = reinterpret_cast<uint32_t*>(vbuf + e * ld + h * 128 + off);
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      vb[(long)e * page] = (uint16_t)((vv.w[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+    for (int w = 0; w < 4; ++w) vl[w] = vv.w[w];
+  }
+  __syncthreads();
+  // V^T: work item = (head, d, entry), entry fastest
+  const int items = row_elems * kScatterRows;
+  for (int t = tid; t < items; t += 256) {
+    const int e = t & (kScatterRows - 1);
+    if (e >= rows) continue;
+    const int hd = t >> 4;  // h * 128 + d
+    const long r = dst[i0 + e];
+    const long pg = r / page, slot = r % page;
+    const int h = hd >> 7, d = hd & 127;
+    v_pool[((pg * n_kv + h) * 128 + d) * page + slot] = vbuf[e * ld + hd];
   }
 }
 
@@ -471,7 +496,9 @@ extern "C" int qh_kv_row_scatter(const void* k_src, const void* v_src, void* k_p
   QH_REQUIRE(n >= 0 && n_kv > 0 && page_tokens > 0, "kv_row_scatter: geometry");
   if (n == 0) return QH_OK;
   QH_REQUIRE(k_src && v_src && k_pool && v_pool && src && dst, "kv_row_scatter: null pointer");
-  hipLaunchKernelGGL(kv_scatter_kernel, dim3(blocks_for(n, 4)), dim3(256), 0,
+  QH_REQUIRE(n_kv <= 15, "kv_row_scatter: n_kv=%d exceeds the 64 KiB staging buffer", n_kv);
+  const size_t smem = (size_t)kScatterRows * (n_kv * 128 + 2) * sizeof(uint16_t);
+  hipLaunchKernelGGL(kv_scatter_kernel, dim3(blocks_for(n, kScatterRows)), dim3(256), smem,
                      (hipStream_t)stream, (const uint16_t*)k_src, (const uint16_t*)v_src,
                      (uint16_t*)k_pool, (uint16_t*)v_pool, src, dst, n, n_kv, page_tokens);
   return launch_status("kv_row_scatter");

@@ -376,6 +376,15 @@ def test_kv_row_scatter_and_copy_bit_exact():
     ref.kv_row_scatter(k_pool_rows, v_pool_rows, k_src, v_src, src, dst)
     assert torch.equal(layout.k_rows(kp.cpu()), k_pool_rows)
     assert torch.equal(layout.v_rows(vp.cpu()), v_pool_rows)
+    # runs of consecutive arena rows (a row's fresh tokens) starting mid-page,
+    # in page order 9, 3, 17: the coalesced V^T writes of one page row
+    run = torch.cat([torch.arange(9 * 16 + 5, 10 * 16), torch.arange(3 * 16, 4 * 16),
+                     torch.arange(17 * 16, 17 * 16 + 9)])
+    src2 = torch.randperm(T, generator=g)[:run.numel()]
+    K.kv_row_scatter(k_src.to(DEV), v_src.to(DEV), kp, vp, src2.to(DEV), run.to(DEV))
+    ref.kv_row_scatter(k_pool_rows, v_pool_rows, k_src, v_src, src2, run)
+    assert torch.equal(layout.k_rows(kp.cpu()), k_pool_rows)
+    assert torch.equal(layout.v_rows(vp.cpu()), v_pool_rows)
     # pool -> pool copy (tail of a kept page into a temporary)
     csrc = torch.randperm(rows, generator=g)[:30]
     cdst = torch.randperm(rows, generator=g)[:30]
