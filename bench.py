@@ -49,7 +49,11 @@ class KernelClock:
         e0.record()
         out = launch()
         e1.record()
-        self.gemm.append((2.0 * M * N * K, e0, e1, name))
+        # algorithmic HBM bytes: A, B and their scales once, the output once
+        # (bf16, or e4m3 + scales for the fused gate_up)
+        out_bytes = (M * (N // 2) + M * (N // 256) * 4) if name == "gate_up" else 2 * M * N
+        nbytes = M * K + N * K + M * (K // 128) * 4 + (N // 128) * (K // 128) * 4 + out_bytes
+        self.gemm.append((2.0 * M * N * K, e0, e1, name, nbytes))
         return out
 
     def attention_hook(self, kind, pairs, kv_rows, n_queries, launch):
@@ -73,16 +77,17 @@ class KernelClock:
     def summary(self):
         self.torch.cuda.synchronize()
         g_flops = sum(x[0] for x in self.gemm)
+        g_bytes = sum(x[4] for x in self.gemm)
         g_ms = sum(x[1].elapsed_time(x[2]) for x in self.gemm)
         per_shape = {}
-        for flops, e0, e1, name in self.gemm:
+        for flops, e0, e1, name, _ in self.gemm:
             f, t, n = per_shape.get(name, (0.0, 0.0, 0))
             per_shape[name] = (f + flops, t + e0.elapsed_time(e1), n + 1)
         a_flops = sum(x[0] for x in self.attn)
         a_bytes = sum(x[1] for x in self.attn)
         a_ms = sum(x[2].elapsed_time(x[3]) for x in self.attn)
         return dict(
-            gemm_launches=len(self.gemm), gemm_ms=g_ms, gemm_flops=g_flops,
+            gemm_launches=len(self.gemm), gemm_ms=g_ms, gemm_flops=g_flops, gemm_bytes=g_bytes,
             gemm_tflops=g_flops / g_ms / 1e9 if g_ms else 0.0,
             gemm_shapes={k: dict(launches=n, ms=round(t, 3),
                                  tflops=round(f / t / 1e9, 1) if t else 0.0)
@@ -127,6 +132,38 @@ def cpu_baseline(model, spec, instruction, documents, tail, rows, threads):
                 tokens=chunk.tokens, bits=bits.tolist(), margins=margins.tolist())
 
 
+def copy_calibration(nbytes):
+    """A plain elementwise copy kernel that reads and writes `nbytes` each."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": src.numel() * 4, "dispatches": 3}), flush=True)
+
+
+# HBM bytes per GEMM launch measured with rocprofv3 counters on this same
+# workload (FETCH_SIZE and WRITE_SIZE passes, scaled by a copy kernel of
+# known size); the profile summary records the commands and the factors.
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_fp8_aiif_qwen3_4b_hbm_traffic.md")
+
+
+def measured_gemm_traffic():
+    """(bytes per launch, source) from the committed counter profile, or (None, reason)."""
+    import re
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            text = f.read()
+    except OSError:
+        return None, "no counter profile"
+    m = re.search(r"gemm_hbm_bytes_per_launch\s*=\s*([0-9.eE+]+)", text)
+    if not m:
+        return None, "counter profile has no gemm_hbm_bytes_per_launch line"
+    return float(m.group(1)), os.path.relpath(TRAFFIC_PROFILE, ROOT)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -139,7 +176,13 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES (fp32 x * 1) three times: "
+                         "the known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): this build has no "
               f"multi-GPU path; rows shard per GPU with no device communication.",
@@ -207,6 +250,7 @@ def main():
             cpu = {"value": None, "unit": "rows/s", "cores": 0, "kind": "port",
                    "sample": f"failed: {exc!r}"}
 
+    traffic, traffic_src = measured_gemm_traffic()
     line = {
         "metric": "rows/s + prefill tok/s, Qwen3-4B fp8 AI.IF on 1 GPU; attn/GEMM % of MFMA peak",
         "value": round(rows_per_s, 2), "unit": "rows/s", "n_gpus": 1,
@@ -225,7 +269,11 @@ def main():
         "input_tok_per_s": round(input_tok_s, 1),
         "roofline": {"bound": "mfma", "achieved": round(k["gemm_tflops"], 1),
                      "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(k["gemm_tflops"] / FP8_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(k["gemm_tflops"] / FP8_PEAK_TFLOPS, 4),
+                     "traffic": traffic,
+                     "traffic_unit": "HBM bytes per GEMM launch (rocprofv3 counters)",
+                     "traffic_source": traffic_src,
+                     "algorithmic_bytes_per_launch": round(k["gemm_bytes"] / max(1, k["gemm_launches"])),
                      "kernel": ("qh fp8_gemm_kernel: qkv, o, down (bf16 out) and gate_up "
                                 "(fused SiLU gate + fp8 quant epilogue)")},
         "gemm": {"share_of_step": round(k["gemm_ms"] / (ms_per_step * args.steps), 3),

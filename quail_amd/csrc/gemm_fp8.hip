@@ -51,7 +51,6 @@ constexpr int NS = 4;           // weight stages in LDS
 constexpr int PA = 2;           // activation blocks in flight ahead
 constexpr int STAGE = BR * BK;  // 32 KiB
 constexpr int LOADS = 12;       // vector-memory loads per wave per step
-constexpr int GROUP_M = 8;
 constexpr int XCDS = 8;
 enum { kStoreBf16 = 0, kSiluQuant = 1 };
 }  // namespace gemm
@@ -68,6 +67,7 @@ struct GemmArgs {
   float* scales;  // kSiluQuant: [N/256, M]
   int M, N, K;
   int ue8m0;
+  int group_m;    // tile rows per column sweep (see launch_gemm)
 };
 
 // Raw buffer descriptor: byte-addressed, `bytes` long; accesses past the end
@@ -109,12 +109,13 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
   const int my_tiles = (n_tiles - (int)blockIdx.x + G - 1) / G;
 
   // linear tile t -> (tile row, tile column): XCD-contiguous chunks, then
-  // GROUP_M tile rows per column sweep
+  // group_m tile rows per column sweep
+  const int group_m = p.group_m;
   auto coords = [&](int t, int& tm, int& tn) __attribute__((always_inline)) {
     if (t < per_xcd * XCDS) t = (t % XCDS) * per_xcd + t / XCDS;
-    const int in_group = GROUP_M * tiles_n;
-    const int first_m = (t / in_group) * GROUP_M;
-    const int gsize = min(tiles_m - first_m, GROUP_M);
+    const int in_group = group_m * tiles_n;
+    const int first_m = (t / in_group) * group_m;
+    const int gsize = min(tiles_m - first_m, group_m);
     tm = first_m + (t % in_group) % gsize;
     tn = (t % in_group) / gsize;
   };
@@ -426,10 +427,18 @@ static int device_cus() {
   return cached[dev];
 }
 
+// Tile order. Each XCD's 32 CUs run 32 consecutive tiles of its chunk at a
+// time, group_m tile rows x 32/group_m tile columns. A wave of tiles re-reads
+// its weight blocks from beyond L2 once per group of tile rows and its
+// activation blocks once per wave of tile columns. group_m = 4 (4 x 8 tiles)
+// was the measured best or within 2 % of it among 1/2/4/8/16 for every
+// Qwen3-4B projection at 102,400 tokens, the fused gate_up included.
 template <int EPI>
-static int launch_gemm(const GemmArgs& a, qh_stream_t stream, const char* what) {
-  const int tiles = ((a.M + gemm::BM - 1) / gemm::BM) * (a.N / gemm::BR);
+static int launch_gemm(GemmArgs a, qh_stream_t stream, const char* what) {
+  const int tiles_n = a.N / gemm::BR;
+  const int tiles = ((a.M + gemm::BM - 1) / gemm::BM) * tiles_n;
   const int grid = min(tiles, device_cus());
+  a.group_m = 4;
   hipLaunchKernelGGL(fp8_gemm_kernel<EPI>, dim3(grid), dim3(512), 0, (hipStream_t)stream, a);
   return launch_status(what);
 }
@@ -457,7 +466,7 @@ extern "C" int qh_fp8_gemm_nt(const void* A, long lda, const float* sa, const vo
   if (M == 0) return QH_OK;
   QH_REQUIRE(A && sa && B && sb && C, "fp8_gemm_nt: null pointer");
   GemmArgs a{(const uint8_t*)A, lda, sa, (const uint8_t*)B, ldb, sb, C, ldc, nullptr,
-             M, N, K, 0};
+             M, N, K, 0, 0};
   return launch_gemm<gemm::kStoreBf16>(a, stream, "fp8_gemm_nt");
 }
 
@@ -476,6 +485,6 @@ extern "C" int qh_fp8_gemm_silu_quant(const void* A, long lda, const float* sa,
   if (M == 0) return QH_OK;
   QH_REQUIRE(A && sa && B && sb && out_q && scales, "fp8_gemm_silu_quant: null pointer");
   GemmArgs a{(const uint8_t*)A, lda, sa, (const uint8_t*)B, ldb, sb, out_q, ld_out, scales,
-             M, 2 * I, K, ue8m0};
+             M, 2 * I, K, ue8m0, 0};
   return launch_gemm<gemm::kSiluQuant>(a, stream, "fp8_gemm_silu_quant");
 }
