@@ -1,4 +1,7 @@
-// Varlen paged attention on bf16 MFMA (gfx950 v_mfma_f32_32x32x16_bf16).
+// Varlen attention on bf16 MFMA (gfx950 v_mfma_f32_32x32x16_bf16).
+//
+// attn_fwd_kernel serves the contiguous-row call (tree call A: K/V are the
+// chunk's own rows); attn_paged_kernel further down serves the paged calls.
 //
 // One workgroup = one q-tile of 32 query rows of one sequence x 4 query heads
 // that share one KV head (GQA packs the 4 heads into the 4 waves, so each K/V
@@ -9,10 +12,8 @@
 //   O^T += V^T P^T (M = head dim, N = queries, K = keys): P^T comes straight
 //                 from the S^T registers (a fixed key permutation inside each
 //                 16-key step, mirrored when V^T fragments are read).
-// K tiles are staged in LDS as [key][d]; V tiles as V^T [d][key]. The arena
-// stores V pages already transposed, so the paged gather is a straight copy of
-// 4 KiB page blocks with 16-byte loads; contiguous (chunk-row) V is transposed
-// on its way into LDS.
+// K tiles are staged in LDS as [key][d]; V tiles as V^T [d][key] (the row
+// V is transposed on its way into LDS).
 #include "common.h"
 
 namespace qh {
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(1024) void attn_tile_scan_kernel(
   if (threadIdx.x == 0) tile_off[n_seqs] = carry;
 }
 
-template <bool PAGED, bool CAUSAL>
+template <bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
   using namespace attn;
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[BKV * K_LD];
@@ -179,35 +180,18 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
     const int key0 = kt * BKV;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      // K: instruction i covers keys 16i .. 16i+15 (one page when paged)
+      // instruction i covers keys 16i .. 16i+15 of the tile
       const int key = key0 + 16 * i + (tid >> 4);
       const int kc = (tid & 15) * 8;
       bf16x8 kv;
       kv.w[0] = kv.w[1] = kv.w[2] = kv.w[3] = 0;
       bf16x8 vv;
       vv.w[0] = vv.w[1] = vv.w[2] = vv.w[3] = 0;
-      if (PAGED) {
-        const int pidx = (key0 >> 4) + i;  // page index within the sequence
-        const bool page_live = pidx * PAGE < kv_end;
-        int page = page_live ? p.table[(long)s * p.table_width + pidx] : -1;
-        if (page >= p.pool_pages) page = -1;
-        if (page >= 0) {
-          const long blk = ((long)page * p.n_kv + hk) * (PAGE * D);
-          if (key < kv_end) kv = load8(p.k_pool + blk + (tid >> 4) * D + kc);
-          // V^T page block [D][PAGE]: chunk tid covers d = tid/2, slots 8*(tid&1)..
-          vv = load8(p.v_pool + blk + (long)tid * 8);
-          const int slot0 = pidx * PAGE + 8 * (tid & 1);
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (slot0 + e >= kv_end) vv.set(e, 0);
-        }
-      } else {
-        if (key < kv_end) {
-          const long row = (long)p.cu_k[s] + key;
-          if (row >= 0 && row < p.kv_rows_total) {
-            kv = load8(p.k_rows + (row * p.n_kv + hk) * D + kc);
-            vv = load8(p.v_rows + (row * p.n_kv + hk) * D + kc);
-          }
+      if (key < kv_end) {
+        const long row = (long)p.cu_k[s] + key;
+        if (row >= 0 && row < p.kv_rows_total) {
+          kv = load8(p.k_rows + (row * p.n_kv + hk) * D + kc);
+          vv = load8(p.v_rows + (row * p.n_kv + hk) * D + kc);
         }
       }
       kreg[i] = kv;
@@ -220,18 +204,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
       const int key = 16 * i + (tid >> 4);
       const int kc = (tid & 15) * 8;
       store8(k_lds + key * K_LD + kc, kreg[i]);
-      if (PAGED) {
-        const int d = tid >> 1;
-        uint2* dstp = reinterpret_cast<uint2*>(vt_lds + d * VT_LD + 16 * i + 8 * (tid & 1));
-        dstp[0] = make_uint2(vreg[i].w[0], vreg[i].w[1]);
-        dstp[1] = make_uint2(vreg[i].w[2], vreg[i].w[3]);
-      } else {
-        // row-layout V: 8 consecutive d of one key, transposed into V^T
+      // row-layout V: 8 consecutive d of one key, transposed into V^T
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          vt_lds[(kc + e) * VT_LD + key] =
-              (uint16_t)((vreg[i].w[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
-      }
+      for (int e = 0; e < 8; ++e)
+        vt_lds[(kc + e) * VT_LD + key] =
+            (uint16_t)((vreg[i].w[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
     }
   };
 
@@ -742,8 +719,8 @@ static int attention_launch(const void* q, long ldq, int q_rows_total, const int
       else hipLaunchKernelGGL((attn_paged_kernel<false, false>), grid, dim3(256), 0, st, p);
     }
   } else {
-    if (causal) hipLaunchKernelGGL((attn_fwd_kernel<false, true>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((attn_fwd_kernel<false, false>), grid, dim3(256), 0, st, p);
+    if (causal) hipLaunchKernelGGL((attn_fwd_kernel<true>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((attn_fwd_kernel<false>), grid, dim3(256), 0, st, p);
   }
   return launch_status("attention");
 }

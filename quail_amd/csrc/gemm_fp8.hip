@@ -24,10 +24,11 @@
 //   - every wave issues exactly LOADS = 12 vector-memory loads per step, all
 //     as inline asm, one between consecutive MFMA pairs; the wait at the top
 //     of step s is vmcnt(12): the loads issued since step s's activations
-//     are exactly the previous step's twelve. The count ignores the stores
-//     of an epilogue in between: stores may complete out of order with
-//     loads, and counting only loads stays correct either way (it can only
-//     wait longer, for stores issued at the end of the step before).
+//     are exactly the previous step's twelve. A wait counts stores too, and
+//     stores may complete out of order with loads, so the count is never
+//     raised for them: a tile's epilogue takes the next step's wait before
+//     it issues its stores, the next step skips its wait, and the stores
+//     have that whole step to drain before the following wait.
 //   - one barrier per step: it publishes stage s (every wave's DMA share has
 //     landed) and frees stage s-1 for the DMA of step s+3. The first two
 //     weight fragments of step s+1 are read at the end of step s.
@@ -50,6 +51,7 @@ constexpr int BK = 128;         // K block: one MFMA, one scale block
 constexpr int NS = 4;           // weight stages in LDS
 constexpr int PA = 2;           // activation blocks in flight ahead
 constexpr int STAGE = BR * BK;  // 32 KiB
+constexpr int EPI_BYTES = 2304; // per-wave LDS slice for staging epilogue stores
 constexpr int LOADS = 12;       // vector-memory loads per wave per step
 constexpr int XCDS = 8;
 enum { kStoreBf16 = 0, kSiluQuant = 1 };
@@ -90,7 +92,8 @@ __device__ __forceinline__ float silu_mul_bf16(float gate_acc, float up_acc) {
 template <int EPI>
 __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
   using namespace gemm;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE];
+  // weight stages, then one epilogue slice per wave
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE + 8 * EPI_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -249,33 +252,57 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
   float sav[PA + 1][2], sbv[PA + 1][2];
 
   // ---- epilogues --------------------------------------------------------------
+  // A lane holds 4 consecutive columns of one token per n-tile, so storing
+  // straight from registers writes 16 scattered 32-byte pieces per
+  // instruction, which measured ~16k cycles per tile. Instead each wave
+  // stages a few rows of its output at a time in its own LDS slice (rows
+  // padded so that the writes are bank-conflict free) and stores whole rows,
+  // 16 bytes per lane.
+  uint8_t* slice = lds + NS * STAGE + wave * EPI_BYTES;
   auto store_bf16 = [&](const Cursor& c) __attribute__((always_inline)) {
-    uint16_t* C = (uint16_t*)p.C;
+    constexpr int ROWB = 512 + 32;  // one 256-column bf16 row + pad
+    uint8_t* C = (uint8_t*)p.C;
+    const long ldc_b = p.ldc * 2;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int m = c.tm * BM + 32 * wave + 16 * j + (lane & 15);
+    for (int pass = 0; pass < 8; ++pass) {
+      // rows 4*pass .. +3 of the wave's 32: token half j = pass / 4, held by
+      // the lanes with (lane % 16) / 4 == pass % 4, row r = lane % 4
+      const int j = pass >> 2;
+      if (((lane & 15) >> 2) == (pass & 3)) {
+        uint8_t* w = slice + (lane & 3) * ROWB + 8 * g;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        // v_cvt_pk_bf16_f32: round-to-nearest-even, as f32_to_bf16
-        const bf16x2 p0 = {(__bf16)acc[i][j][0], (__bf16)acc[i][j][1]};
-        const bf16x2 p1 = {(__bf16)acc[i][j][2], (__bf16)acc[i][j][3]};
-        if (m < M) {
-          const int n = c.tn * BR + 16 * i + 4 * g;
-          *reinterpret_cast<uint2*>(C + (long)m * p.ldc + n) =
+        for (int i = 0; i < 16; ++i) {
+          // v_cvt_pk_bf16_f32: round-to-nearest-even, as f32_to_bf16
+          const bf16x2 p0 = {(__bf16)acc[i][j][0], (__bf16)acc[i][j][1]};
+          const bf16x2 p1 = {(__bf16)acc[i][j][2], (__bf16)acc[i][j][3]};
+          *reinterpret_cast<uint2*>(w + 32 * i) =
               make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
         }
-        acc[i][j] = zero;
+      }
+      // two rows per instruction: lanes 0-31 row 2q, lanes 32-63 row 2q+1
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int R = 2 * q + (lane >> 5), chunk = lane & 31;
+        const uint4 v = *reinterpret_cast<const uint4*>(slice + R * ROWB + chunk * 16);
+        const int m = c.tm * BM + 32 * wave + 4 * pass + R;
+        if (m < M)
+          *reinterpret_cast<uint4*>(C + (long)m * ldc_b + (long)c.tn * BR * 2 + chunk * 16) = v;
       }
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = zero;
   };
   // silu(gate) * up for the tile's 128 output columns 128*tn .. (n-tiles 0-7
   // hold gate, 8-15 the matching up), one 1x128 quantization group per token:
   // a token's 128 values sit in the four lanes lane%16 + 16*g'.
   auto store_silu_quant = [&](const Cursor& c) __attribute__((always_inline)) {
+    constexpr int ROWB = 128 + 16;  // one 128-column e4m3 row + pad
     uint8_t* out = (uint8_t*)p.C;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int m = c.tm * BM + 32 * wave + 16 * j + (lane & 15);
+      const int m_row = c.tm * BM + 32 * wave + 16 * j;
       float amax = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i)
@@ -288,17 +315,25 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
       amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
       amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
       const float scale = group_scale(amax, p.ue8m0 != 0);
+      uint8_t* w = slice + (lane & 15) * ROWB + 4 * g;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        uint32_t w = 0;
+        uint32_t b = 0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) w |= quant_e4m3(acc[i][j][r], scale) << (8 * r);
-        if (m < M)
-          *reinterpret_cast<uint32_t*>(out + (long)m * p.ldc + 128 * c.tn + 16 * i + 4 * g) = w;
+        for (int r = 0; r < 4; ++r) b |= quant_e4m3(acc[i][j][r], scale) << (8 * r);
+        *reinterpret_cast<uint32_t*>(w + 16 * i) = b;
         acc[i][j] = zero;
         acc[i + 8][j] = zero;
       }
-      if (g == 0 && m < M) p.scales[(long)c.tn * M + m] = scale;
+      if (g == 0 && m_row + (lane & 15) < M) p.scales[(long)c.tn * M + m_row + (lane & 15)] = scale;
+      // the 16 staged rows, eight whole 128-byte rows per instruction
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int R = 8 * q + (lane >> 3), chunk = lane & 7;
+        const uint4 v = *reinterpret_cast<const uint4*>(slice + R * ROWB + chunk * 16);
+        if (m_row + R < M)
+          *reinterpret_cast<uint4*>(out + (long)(m_row + R) * p.ldc + 128 * c.tn + chunk * 16) = v;
+      }
     }
   };
   auto epilogue = [&](const Cursor& c) __attribute__((always_inline)) {
@@ -332,14 +367,17 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
   v8i bf = frag(lds, 0), bn = frag(lds, 1);
   f32x4 tp = zero;
   float s_last = 0.f;
+  bool stored = false;  // the previous step ended with an epilogue
 
   auto step = [&](auto slot_c, int s) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
     constexpr int nslot = (slot + PA) % (PA + 1);
     // step s's activations and scales (issued at step s-2) have landed, and
     // with them this wave's DMA share of stage s (issued at s-3); the twelve
-    // loads of step s-1 may be in flight
-    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    // loads of step s-1 may be in flight. After a tile's epilogue that wait
+    // already ran, before the stores were issued (see below).
+    if (!stored) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    stored = false;
     asm volatile(""
                  : "+v"(alo[slot][0]), "+v"(alo[slot][1]), "+v"(ahi[slot][0]),
                    "+v"(ahi[slot][1]), "+v"(sav[slot][0]), "+v"(sav[slot][1]),
@@ -395,7 +433,13 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
       for (int r = 0; r < 4; ++r) acc[15][1][r] += tp[r] * s_last;
       tp = zero;
       s_last = 0.f;
+      // A wait counts stores as well as loads, so the epilogue's stores would
+      // hold up the next step's wait until they complete. Take that wait now,
+      // while no store is outstanding, and skip it at the next step: the
+      // stores then have a whole step to drain before the wait after that.
+      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
       epilogue(cc);
+      stored = true;
     }
     advance(cc);
     advance(ca);
