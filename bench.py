@@ -169,7 +169,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--rows", type=int, default=4096)
+    ap.add_argument("--workload", default="aiif-4b", choices=["aiif-4b", "aiif-32b"],
+                    help="aiif-4b: Qwen3-4B, 64-token instruction, lognormal docs (median "
+                         "180, cap 1024); aiif-32b: Qwen3-32B, 128-token instruction, docs "
+                         "uniform in [1024, 4096]")
+    ap.add_argument("--rows", type=int, default=None,
+                    help="rows (default 4096 for aiif-4b, 256 for aiif-32b)")
     ap.add_argument("--layers", type=int, default=None)
     ap.add_argument("--attention", default="unified", choices=["unified", "tree"])
     ap.add_argument("--arena-pages", type=int, default=None)
@@ -194,14 +199,24 @@ def main():
     from quail_amd import budgets
     from quail_amd.aiif import FilterRunner, synthetic_filter_workload
     from quail_amd.model import build_random_qwen3
-    from quail_amd.specs import MI355X, QWEN3_4B_FP8
+    from quail_amd.specs import MI355X, QWEN3_32B_FP8, QWEN3_4B_FP8
     from dataclasses import replace
 
-    spec = QWEN3_4B_FP8 if args.layers is None else replace(QWEN3_4B_FP8, layers=args.layers)
+    big = args.workload == "aiif-32b"
+    if args.rows is None:
+        args.rows = 256 if big else 4096
+    base = QWEN3_32B_FP8 if big else QWEN3_4B_FP8
+    spec = base if args.layers is None else replace(base, layers=args.layers)
     t_build = time.perf_counter()
-    model = build_random_qwen3(spec, seed=args.seed, device="cuda", max_pos=2048)
-    instruction, documents, tail = synthetic_filter_workload(args.rows, seed=args.seed,
-                                                             vocab=spec.vocab)
+    model = build_random_qwen3(spec, seed=args.seed, device="cuda",
+                               max_pos=8192 if big else 2048)
+    if big:
+        instruction, documents, tail = synthetic_filter_workload(
+            args.rows, prefix_tokens=128, uniform_lengths=(1024, 4096), seed=args.seed,
+            vocab=spec.vocab)
+    else:
+        instruction, documents, tail = synthetic_filter_workload(args.rows, seed=args.seed,
+                                                                 vocab=spec.vocab)
     clock = KernelClock(torch)
     clock.n_q, clock.d, clock.n_kv = spec.n_q, spec.d_head, spec.n_kv
     runner = FilterRunner(model, spec, device_spec=MI355X, n_pages=args.arena_pages,
@@ -233,7 +248,11 @@ def main():
     steady = all(r[0] == answers for r in results)
 
     cpu = None
-    if not args.no_cpu_baseline and args.cpu_rows > 0:
+    if big and not args.no_cpu_baseline:
+        # one 32B row of 1-4 k tokens is ~0.2 PFLOP: minutes on the host cores
+        cpu = {"value": None, "unit": "rows/s", "cores": 0, "kind": "port",
+               "sample": "not run for the Qwen3-32B workload (one row is minutes of CPU)"}
+    elif not args.no_cpu_baseline and args.cpu_rows > 0:
         threads = min(16, len(os.sched_getaffinity(0)))
         try:
             base = cpu_baseline(model, spec, instruction, documents, tail, args.cpu_rows,
@@ -250,17 +269,24 @@ def main():
             cpu = {"value": None, "unit": "rows/s", "cores": 0, "kind": "port",
                    "sample": f"failed: {exc!r}"}
 
-    traffic, traffic_src = measured_gemm_traffic()
+    if big:   # the counter profile covers the Qwen3-4B workload only
+        traffic, traffic_src = None, "not measured for this workload"
+    else:
+        traffic, traffic_src = measured_gemm_traffic()
     line = {
-        "metric": "rows/s + prefill tok/s, Qwen3-4B fp8 AI.IF on 1 GPU; attn/GEMM % of MFMA peak",
+        "metric": (f"rows/s + prefill tok/s, {'Qwen3-32B' if big else 'Qwen3-4B'} fp8 AI.IF "
+                   f"on 1 GPU; attn/GEMM % of MFMA peak"),
         "value": round(rows_per_s, 2), "unit": "rows/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 1),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8",
         "data": "synthetic",
-        "config": {"workload": (f"AI.IF filter, Qwen3-4B-arch fp8 random init, "
-                                f"{spec.layers} layers, {args.rows} rows, 64-token shared "
-                                f"instruction, lognormal docs (median 180, cap 1024), "
-                                f"24-token tail, {args.attention} attention"),
+        "config": {"workload": (
+                       f"AI.IF filter, {'Qwen3-32B' if big else 'Qwen3-4B'}-arch fp8 random "
+                       f"init, {spec.layers} layers, {args.rows} rows, "
+                       + ("128-token shared instruction, docs uniform in [1024, 4096]"
+                          if big else "64-token shared instruction, lognormal docs "
+                                      "(median 180, cap 1024)")
+                       + f", 24-token tail, {args.attention} attention"),
                    "rows": args.rows, "layers": spec.layers,
                    "fresh_tokens": stats["fresh_tokens"],
                    "input_tokens": stats["input_tokens"], "chunks": stats.get("chunks"),

@@ -30,17 +30,22 @@ def lognormal_lengths(n, median, mean, cap, rng):
 
 
 def synthetic_filter_workload(n_rows, *, prefix_tokens=64, median=180, mean=230,
-                              cap=1024, tail_tokens=24, vocab=151_936, seed=0):
+                              cap=1024, tail_tokens=24, vocab=151_936, seed=0,
+                              uniform_lengths=None):
     """Rows of an AI.IF over a Qwen3-sized vocabulary.
 
     Every row is a shared `prefix_tokens`-token instruction, then a
-    document of lognormal length (median, mean, capped) of uniform random
-    ids; one question tail of `tail_tokens` ids follows each row.
+    document of uniform random ids whose length is lognormal (median, mean,
+    capped) or, with uniform_lengths=(lo, hi), uniform in [lo, hi]; one
+    question tail of `tail_tokens` ids follows each row.
     Returns (instruction ids, documents, question tail).
     """
     rng = np.random.default_rng(seed)
     instruction = rng.integers(0, vocab, size=prefix_tokens, dtype=np.int64)
-    lens = lognormal_lengths(n_rows, median, mean, cap, rng)
+    if uniform_lengths is None:
+        lens = lognormal_lengths(n_rows, median, mean, cap, rng)
+    else:
+        lens = rng.integers(uniform_lengths[0], uniform_lengths[1] + 1, size=n_rows)
     documents = [rng.integers(0, vocab, size=int(L), dtype=np.int64) for L in lens]
     tail = rng.integers(0, vocab, size=tail_tokens, dtype=np.int64)
     return instruction, documents, tail

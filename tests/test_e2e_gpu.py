@@ -93,6 +93,56 @@ def test_every_layer_matches_the_oracle_teacher_forced(path):
 
 
 @pytest.mark.parametrize("path", ["unified", "tree"])
+def test_qwen3_32b_geometry_layers_match_the_oracle(path):
+    """The Qwen3-32B layer geometry (hidden 5120, 64 query / 8 KV heads = GQA
+    8:1, FFN 25,600: GEMMs (10240|5120|51200|5120) x (5120|8192|5120|25600))
+    through two layers, teacher-forced against the oracle with the same bars."""
+    from quail_amd.specs import QWEN3_32B_FP8
+    spec = replace(QWEN3_32B_FP8, layers=2, vocab=4096, tied_head=True)
+    model = build_random_qwen3(spec, seed=5, device="cuda", max_pos=2048,
+                               answer_token_ids=TINY_TRUE + TINY_FALSE)
+    docs, tail = tiny_workload(seed=6, n_rows=10, max_doc=80)
+    pages = 120
+    arena = KVArena(spec.layers, pages, 16, spec.n_kv, spec.d_head, device="cuda")
+    pipe = Qwen3Pipeline(model, arena, spec=spec)
+    traces, hosts = [], []
+
+    def trace(layer, hidden, residual):
+        traces[-1].append((hidden.float().cpu(),
+                           None if residual is None else residual.float().cpu()))
+
+    class Rec:
+        tree_attention, canvas_ids, needs_pages = True, (), False
+
+        def forward_chunk(self, chunk):
+            traces.append([])
+            hosts.append((chunk.host, chunk.attention_mode))
+            return pipe.forward_chunk(chunk)
+
+    pipe.trace = trace
+    ans = AsyncAnswers(torch, AnswerRows(torch, model, TINY_TRUE, TINY_FALSE))
+    stream = loop.FilterStream(torch, arena, Rec(), ans, docs, [list(tail)], 400,
+                               arena_writes=True, attention_mode=path,
+                               prefix_tree=prefix_tree(docs, 16))
+    while not stream.done:
+        stream.next()
+    assert stream.chunks >= 2 and stream.sched.borrowing.borrowed_tokens > 0
+    w = oforward.cpu_weights(model)
+    oarena = oforward.OracleArena(spec.layers, pages, spec.n_kv, spec.d_head)
+    for (host, mode), layers in zip(hosts, traces):
+        for li, L in enumerate(w["layers"]):
+            h_in, r_in = layers[li]
+            h_in = h_in.to(torch.bfloat16)
+            r_in = None if r_in is None else r_in.to(torch.bfloat16)
+            h_ref, r_ref = oforward.layer_step(L, li, h_in, r_in, host, mode, oarena)
+            h_gpu, r_gpu = layers[li + 1]
+            worst = ((h_gpu - h_ref.float()).norm(dim=1)
+                     / h_ref.float().norm(dim=1).clamp(min=1e-6)).max().item()
+            rec = (li, _rel(h_gpu, h_ref), worst, _rel(r_gpu, r_ref))
+            assert rec[1] < 0.08 and rec[2] < 0.20 and rec[3] < 0.02, f"layer {rec}"
+
+
+@pytest.mark.parametrize("path", ["unified", "tree"])
 def test_decisions_agree_outside_the_noise_band(path):
     model = build_random_qwen3(TINY, seed=3, device="cuda", max_pos=2048,
                                answer_token_ids=TINY_TRUE + TINY_FALSE)
