@@ -9,14 +9,18 @@ every array of a chunk reaches the GPU in one pinned H2D copy.
 
 FilterStream / run_filter drive the filter: admit, activate pages, pack,
 launch the forward pass, and read the previous chunk's answers while the
-current one runs (loop.py:1195-1559).
+current one runs (loop.py:1195-1559). run_join drives a join the same way
+over JoinAdmission's groups (loop.py:609-976).
 """
 
+import logging
 import time
 
 import numpy as np
 
-from quail_amd.pack import FilterAdmission
+from quail_amd.pack import FilterAdmission, JoinAdmission, partner_pages
+
+logger = logging.getLogger(__name__)
 
 ATTENTION_PATHS = ("unified", "tree")
 
@@ -536,6 +540,14 @@ class FilterStream:
                     f=len(self.doc_ids[doc]) + self.preamble,
                     suffixes=[self.tails[stage]])
 
+    def set_reserve(self, pages):
+        """Keep `pages` free for a join consumer's partner rows (loop.py:1361-1374)."""
+        for doc, ids in enumerate(self.doc_ids):
+            if self.arena.page_cost(len(ids) + self.capacity_extra) + pages > self.arena.n_pages:
+                raise ValueError(f"document {doc} needs more pages than the arena holds "
+                                 f"beside the join's {pages} pages of partner rows")
+        self.reserve_pages = pages
+
     def _activate(self, doc):
         borrowing = self.sched.borrowing
         key = self.keys[doc]
@@ -676,3 +688,301 @@ def run_filter(torch, arena, pipeline, async_ans, doc_ids, question_ids, budget,
         stats["borrowed_tokens"] = stream.sched.borrowing.borrowed_tokens
         stats["chunks"] = stream.chunks
     return stream.answers, stream.spans, stream.tokens
+
+
+# ------------------------------------------------------------------ the join
+
+
+class _JoinDriver:
+    """State of one run_join call: the scheduler, the arena keys, launches in flight."""
+
+    def __init__(self, torch, arena, pipeline, async_ans, prefixes, keys, stage_suffixes,
+                 budget, frames, anchor_done, anchor_source, anchor_partners, anchor_batch,
+                 staging, mode, prefix_tree):
+        self.torch, self.arena, self.pipeline = torch, arena, pipeline
+        self.async_ans = async_ans
+        self.prefixes, self.keys = prefixes, keys
+        self.stage_suffixes = stage_suffixes
+        self.budget = budget
+        self.frames = frames
+        self.anchor_done = anchor_done
+        self.source = anchor_source
+        self.anchor_partners = anchor_partners
+        self.anchor_batch = anchor_batch
+        self.staging = staging
+        self.mode = mode
+        self.n_stages = len(stage_suffixes)
+        # a frame entry's rows land in the anchor's pages after its document
+        self.frame_max = max(len(f) for f in frames)
+        self.spans = []
+        self.tokens = 0
+        self.outstanding = []          # (groups, readout handle), launch order
+        self.packed_groups = []
+        resident = {a: self.held_pages(keys[a], len(prefixes[a]))
+                    for a in range(len(keys)) if arena.is_resident(keys[a])}
+        # resident anchors stay for the whole join
+        for a in resident:
+            arena.pin(keys[a])
+        self.sched = JoinAdmission(
+            [len(p) for p in prefixes], [[len(s) for s in sufs] for sufs in stage_suffixes],
+            budget, arena.n_pages, arena.page_tokens,
+            frame_tokens=[len(f) for f in frames], resident=resident,
+            anchor_partners={a: self.partners_of(keys[a]) for a in range(len(keys))},
+            temporary_suffix_pages=mode == "unified",
+            answer_dtype=async_ans.dtype, page_cost=arena.page_cost, tree=prefix_tree)
+        borrowing = self.sched.borrowing
+        borrowing.can_borrow = borrow_check(arena, keys, borrowing)
+        # counted after resident anchors detach: they borrow nothing
+        self.borrowers = borrowing.borrowers()
+        self.lowest_borrow = lowest_borrows(borrowing)
+        self.held = [keys[a] for a, n in enumerate(self.borrowers) if n]
+
+    def partners_of(self, key):
+        return None if self.anchor_partners is None else self.anchor_partners(key)
+
+    def held_pages(self, key, prefix_tokens):
+        """Pages a resident anchor already covers of what the scheduler prices."""
+        capacity = prefix_tokens + self.frame_max
+        return self.arena.page_cost(capacity) - self.arena.growth_cost(key, capacity)
+
+    # ---- streamed anchors ------------------------------------------------
+
+    def admit(self, items):
+        arena = self.arena
+        if self.anchor_batch is not None and items:
+            kept = set(self.anchor_batch([key for key, _ in items]))
+            for key, _ in items:
+                if key not in kept and arena.is_resident(key):
+                    arena.free_key(key)
+            items = [(key, prefix) for key, prefix in items if key in kept]
+        for key, prefix in items:
+            if not arena.is_resident(key):
+                raise ValueError(f"streamed anchor {key!r} has no KV in the arena")
+            arena.pin(key)
+            self.keys.append(key)
+            self.prefixes.append(prefix)
+            self.sched.admit(len(prefix), self.held_pages(key, len(prefix)),
+                             partners=self.partners_of(key))
+
+    def pull(self, evict_retained=False, force=False):
+        """Run source chunks until a join chunk can fill or the source blocks."""
+        moved = False
+        source = self.source
+        while not source.done and (force or self.sched.buildable_tokens() < self.budget):
+            force = False
+            before = source.chunks
+            items, blocked = source.next(evict_retained=evict_retained)
+            self.admit(items)
+            moved = moved or bool(items) or source.chunks > before
+            if blocked:
+                break
+        return moved
+
+    # ---- chunks ------------------------------------------------------------
+
+    def entry_rows(self, a, j, start, end, carried):
+        rows = len(self.prefixes[a]) if carried else 0
+        rows += sum(len(self.stage_suffixes[j][i])
+                    for i in self.sched.partner_indices(a, j, start, end))
+        if self.frames[j] and start == 0:
+            rows += len(self.frames[j])
+        return rows
+
+    def specs(self, groups):
+        """pack_chunk groups for one chunk; activates fresh anchors' pages."""
+        arena, sched = self.arena, self.sched
+        borrowing = sched.borrowing
+        out = []
+        for a, j, start, end, carried in groups:
+            key = self.keys[a]
+            f = len(self.prefixes[a])
+            frame = self.frames[j]
+            parent, shared = ((borrowing.parent(a), borrowing.shared(a))
+                              if carried else (None, 0))
+            fresh = not arena.is_resident(key)
+            got = arena.activate(key, f, capacity_tokens=f + self.frame_max, base_tokens=f,
+                                 borrow=(self.keys[parent], shared) if shared else None)
+            assert got is not None, "scheduler admitted an anchor the arena cannot hold"
+            if fresh and a < len(self.borrowers) and self.borrowers[a]:
+                arena.hold(key, self.borrowers[a])
+                arena.keep_window(key, self.lowest_borrow[a])
+            prefix = None
+            if carried:
+                prefix = self.prefixes[a][shared:] if shared else self.prefixes[a]
+            suffixes = [self.stage_suffixes[j][i]
+                        for i in sched.partner_indices(a, j, start, end)]
+            if frame and start == 0:
+                # frame entry: the frame is written into the anchor's KV after
+                # the document (its answer row is read and discarded); the
+                # partners then read document + frame
+                out.append(dict(key=key, prefix=prefix, start=shared, f=f,
+                                suffixes=[frame], write_suffix_tokens=len(frame)))
+                out.append(dict(key=key, prefix=None, f=f + len(frame), suffixes=suffixes))
+            else:
+                out.append(dict(key=key, prefix=prefix, start=shared, f=f + len(frame),
+                                suffixes=suffixes))
+        return out
+
+    def run_part(self, part):
+        """Run one chunk of groups; halve it when its temporary pages do not fit."""
+        try:
+            self.run_one(part)
+        except ArenaFullError as error:
+            need = self.arena.page_cost(sum(self.entry_rows(*g) for g in part))
+            if self.arena.evict_retained(need):
+                logger.info("join chunk of %d groups retried after evicting retained KV",
+                            len(part))
+                self.run_part(part)
+                return
+            if len(part) < 2:
+                raise
+            logger.info("join chunk of %d groups split: %s", len(part), error)
+            half = len(part) // 2
+            self.run_part(part[:half])
+            self.run_part(part[half:])
+
+    def run_one(self, part):
+        torch = self.torch
+        if self.staging is None and str(getattr(self.arena, "device", "cpu")).startswith("cuda"):
+            self.staging = Stager(torch, self.arena.device)
+        chunk = pack_chunk(torch, self.arena, self.specs(part), attention_mode=self.mode,
+                           staging=self.staging)
+        self.packed_groups.append(list(part))
+        self.tokens += chunk.tokens
+        events = None
+        if torch.cuda.is_available() and str(getattr(self.arena, "device", "")).startswith("cuda"):
+            events = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            events[0].record()
+        normed = _forward(self.pipeline, self.arena, chunk)
+        if events is not None:
+            events[1].record()
+        for key in chunk.fresh_keys:
+            self.arena.trim_window(key)
+        self.spans.append((part[0][1],) + (events or (None, None)))
+        self.outstanding.append((part, self.async_ans.submit(normed)))
+        # read the previous chunk's answers while this one runs
+        while len(self.outstanding) > 1:
+            self.report(self.outstanding.pop(0))
+
+    # ---- answers -------------------------------------------------------------
+
+    def settle(self, anchor):
+        if self.anchor_done is None:
+            if self.arena.is_resident(self.keys[anchor]):
+                self.arena.free_key(self.keys[anchor])
+        else:
+            self.anchor_done(anchor, self.sched.answers[self.n_stages - 1].get(anchor, []))
+
+    def event(self, kind, anchor):
+        if kind == "finished":
+            self.settle(anchor)
+        elif self.arena.is_resident(self.keys[anchor]):
+            self.arena.free_key(self.keys[anchor])
+
+    def report(self, entry):
+        groups, handle = entry
+        bits = self.async_ans.result(handle)
+        pos = 0
+        for a, j, start, end, _ in groups:
+            if self.frames[j] and start == 0:
+                pos += 1          # the frame entry's answer row means nothing
+            count = end - start
+            for kind, anchor in self.sched.report(a, j, start, end, bits[pos:pos + count]):
+                self.event(kind, anchor)
+            pos += count
+
+    # ---- the loop ------------------------------------------------------------
+
+    def run(self):
+        sched, arena, source = self.sched, self.arena, self.source
+        while True:
+            if source is not None and not source.done:
+                self.pull()
+            for kind, anchor in sched.take_settled():
+                self.event(kind, anchor)
+            if sched.done() and (source is None or source.done):
+                break
+            if sched.blocked_pages:
+                arena.evict_retained(sched.blocked_pages)
+            groups = sched.next_chunk(arena.free_pages)
+            if not groups:
+                if self.outstanding:
+                    self.report(self.outstanding.pop(0))
+                    continue
+                if source is not None and not source.done:
+                    if self.pull(evict_retained=True, force=True):
+                        continue
+                if sched.blocked_pages and arena.evict_retained(sched.blocked_pages):
+                    continue
+                # parents held for queued children: the children pack whole
+                if arena.drop_holds(self.held):
+                    continue
+                raise AssertionError("nothing buildable and nothing in flight")
+            self.run_part(groups)
+            # packed children hold their parents' pages now
+            tree_parent = sched.borrowing.tree_parent
+            for a, _, start, _, carried in groups:
+                parent = tree_parent[a] if a < len(tree_parent) else None
+                if carried and start == 0 and parent is not None:
+                    arena.release(self.keys[parent])
+        while self.outstanding:
+            self.report(self.outstanding.pop(0))
+        arena.drop_holds(self.held)
+
+
+def run_join(torch, arena, pipeline, async_ans, anchor_prefixes, stage_suffixes, budget,
+             stage_frames=None, anchor_keys=None, anchor_done=None, anchor_source=None,
+             anchor_partners=None, anchor_batch=None, staging=None, attention_mode=None,
+             prefix_tree=None, stats=None):
+    """The join driver: stream every anchor's partners, gating between stages
+    (loop.py:609-976).
+
+    Args follow the reference: anchor_prefixes[a] is anchor a's prefix ids
+    (document, with any shared instruction); stage_suffixes[j] the partner
+    suffix id lists of stage j; stage_frames[j] the framing ids written into
+    the anchor's KV after its document; anchor_keys stable arena keys;
+    anchor_done(a, row) owns a finished anchor's pages; anchor_source a
+    stream (a FilterStream holding its survivors) that hands over resident
+    anchors while the join runs; anchor_partners(key) per-stage partner
+    index lists; anchor_batch(keys) filters streamed anchors; attention_mode
+    "tree" (the default for joins) or "unified"; prefix_tree a PrefixTree
+    over the anchors, so children borrow their parent's pages.
+
+    Returns (answers, spans, tokens): answers[j][a] is anchor a's 0/1 row
+    over its stage-j partners; spans (stage, start event, end event) per
+    forward pass; tokens the fresh tokens packed.
+    """
+    k = len(stage_suffixes)
+    if anchor_source is not None:
+        if anchor_prefixes or anchor_keys:
+            raise ValueError("anchor_source fills anchor_prefixes and anchor_keys")
+        prefixes, keys = anchor_prefixes, anchor_keys
+    else:
+        prefixes = list(anchor_prefixes)
+        keys = list(range(len(prefixes))) if anchor_keys is None else list(anchor_keys)
+    if len(keys) != len(prefixes):
+        raise ValueError("anchor_keys must match anchor_prefixes")
+    if tuple(getattr(pipeline, "canvas_ids", ())):
+        raise ValueError("canvas rows belong to diffusion models, not this build")
+    frames = stage_frames or [[] for _ in range(k)]
+    if k == 0:
+        return [], [], 0
+    # a join's partners read their anchor: tree unless the plan says otherwise
+    mode = attention_path(pipeline, attention_mode, default="tree")
+    if anchor_source is not None and mode == "unified":
+        # leave room for one partner's temporary rows beside held anchors
+        longest = [max((len(s) for s in sufs), default=0) for sufs in stage_suffixes]
+        anchor_source.set_reserve(max(
+            (partner_pages(arena.page_cost, arena.page_tokens, len(doc), len(frame), rows)
+             for doc in anchor_source.doc_ids for frame, rows in zip(frames, longest)),
+            default=0))
+    if prefix_tree is not None and not prefix_tree.shared_tokens:
+        prefix_tree = None
+    driver = _JoinDriver(torch, arena, pipeline, async_ans, prefixes, keys, stage_suffixes,
+                         budget, frames, anchor_done, anchor_source, anchor_partners,
+                         anchor_batch, staging, mode, prefix_tree)
+    driver.run()
+    if stats is not None:
+        stats["borrowed_tokens"] = driver.sched.borrowing.borrowed_tokens
+        stats["chunks"] = len(driver.packed_groups)
+    return driver.sched.answers, driver.spans, driver.tokens

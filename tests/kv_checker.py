@@ -103,7 +103,9 @@ class HashModel:
                 src = written[phys]
                 return ids[src], positions[src], row_hash(src)
             if phys in copied:
-                return self._stored(copied[phys])
+                # the tail copy runs after the scatter: it copies this
+                # chunk's writes where they land on the copied rows
+                return value(copied[phys])
             return self._stored(phys)
 
         def row_hash(row):
@@ -127,10 +129,11 @@ class HashModel:
         for i in range(len(cu) - 1):
             count = cu[i + 1] - cu[i]
             self._chain_ok(lambda v, i=i: value(self._phys(table, i, v)), used[i] - count)
+        copies = {dst: value(src) for dst, src in copied.items()}
         for dst, src in written.items():
             self.token[dst], self.position[dst], self.hash[dst] = ids[src], positions[src], hashes[src]
-        for dst, src in copied.items():
-            self.token[dst], self.position[dst], self.hash[dst] = self._stored(src)
+        for dst, stored in copies.items():
+            self.token[dst], self.position[dst], self.hash[dst] = stored
 
     def _tree(self, h, ids, positions, hashes):
         cu_a = h["cu_a"].tolist()
@@ -226,3 +229,84 @@ def check_filter(docs, questions, *, path, pages=400, budget=600):
     assert not arena.accounting.owned, "the filter left pages resident"
     assert arena.free_pages == pages
     return model, tokens
+
+
+def _arena(pages):
+    return KVArena(n_layers=1, n_pages=pages, page_tokens=16, n_kv=1, d_head=1,
+                   dtype=torch.float32, device="cpu", allocate=False)
+
+
+def join_answers(anchors, frame, partners):
+    """Planted answers of every (anchor, partner) chain, and of each frame entry."""
+    answers = {}
+    for anchor in anchors:
+        answers[chain(list(anchor) + list(frame))] = 0     # frame entry: discarded
+        for partner in partners:
+            hv = chain(list(anchor) + list(frame) + list(partner))
+            answers[hv] = answer(hv)
+    return answers
+
+
+def check_join(anchors, frame, partners, *, path, pages=400, budget=600, retain=False):
+    """Run a join with the product loop; check every pair's answer and KV read.
+
+    With retain, finished anchors stay in the arena as evictable KV that
+    later fresh anchors evict for pages (the reference's
+    tests/kv_checker.py:364-395).
+    """
+    answers = join_answers(anchors, frame, partners)
+    arena = _arena(pages)
+    model = HashModel(arena, answers)
+    keys = [("a", i) for i in range(len(anchors))]
+    if retain:
+        arena.retention_cap_pages = pages
+    rows = {}
+
+    def anchor_done(a, row):
+        rows[a] = list(row)
+        if retain:
+            arena.retain(keys[a], len(anchors[a]))
+        else:
+            arena.free_key(keys[a])
+
+    stats = {}
+    _, _, tokens = loop.run_join(
+        torch, arena, _Pipeline(model), _Passthrough(), anchors, [partners], budget,
+        stage_frames=[frame], anchor_keys=keys, anchor_done=anchor_done,
+        attention_mode=path, prefix_tree=prefix_tree(anchors, 16), stats=stats)
+    for a, anchor in enumerate(anchors):
+        want = [answers[chain(list(anchor) + list(frame) + list(p))] for p in partners]
+        assert rows[a] == want, f"anchor {a}"
+    arena.evict_retained(pages)
+    assert not arena.accounting.owned, "the join left pages resident"
+    assert arena.free_pages == pages
+    return model, tokens, stats
+
+
+def check_feed(docs, question, frame, partners, *, path, pages=400, budget=600):
+    """A filter whose held survivors feed a join as resident anchors
+    (the reference's tests/kv_checker.py:398-424)."""
+    answers = join_answers(docs, frame, partners)
+    for doc in docs:
+        hv = chain(list(doc) + list(question))
+        answers[hv] = answer(hv >> 3)
+    arena = _arena(pages)
+    model = HashModel(arena, answers)
+    source = loop.FilterStream(
+        torch, arena, _Pipeline(model), _Passthrough(), docs, [question], budget,
+        arena_writes=True, arena_keys=[("d", i) for i in range(len(docs))],
+        hold_survivors=True, hold_extra_tokens=len(frame),
+        prefix_tree=prefix_tree(docs, 16), attention_mode=path)
+    keys = []
+    out, _, _ = loop.run_join(
+        torch, arena, _Pipeline(model), _Passthrough(), [], [partners], budget,
+        stage_frames=[frame], anchor_keys=keys, anchor_source=source, attention_mode=path)
+    survivors = {d for d, doc in enumerate(docs)
+                 if answers[chain(list(doc) + list(question))]}
+    assert {key[1] for key in keys} == survivors
+    for a, key in enumerate(keys):
+        doc = docs[key[1]]
+        want = [answers[chain(list(doc) + list(frame) + list(p))] for p in partners]
+        assert out[0][a] == want, f"anchor {key[1]}"
+    assert not arena.accounting.owned
+    return model
