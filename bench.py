@@ -86,7 +86,14 @@ class KernelClock:
         a_flops = sum(x[0] for x in self.attn)
         a_bytes = sum(x[1] for x in self.attn)
         a_ms = sum(x[2].elapsed_time(x[3]) for x in self.attn)
+        kinds = {}
+        for flops, nbytes, e0, e1, kind in self.attn:
+            f, t, n = kinds.get(kind, (0.0, 0.0, 0))
+            kinds[kind] = (f + flops, t + e0.elapsed_time(e1), n + 1)
         return dict(
+            attn_kinds={k: dict(launches=n, ms=round(t, 3),
+                                tflops=round(f / t / 1e9, 1) if t else 0.0)
+                        for k, (f, t, n) in kinds.items()},
             gemm_launches=len(self.gemm), gemm_ms=g_ms, gemm_flops=g_flops, gemm_bytes=g_bytes,
             gemm_tflops=g_flops / g_ms / 1e9 if g_ms else 0.0,
             gemm_shapes={k: dict(launches=n, ms=round(t, 3),
@@ -132,6 +139,45 @@ def cpu_baseline(model, spec, instruction, documents, tail, rows, threads):
                 tokens=chunk.tokens, bits=bits.tolist(), margins=margins.tolist())
 
 
+def cpu_baseline_join(model, spec, anchor, frame, partners, threads):
+    """The CPU oracle forward of one anchor (prefix + frame written once) and
+    its first len(partners) partners, unified attention, one chunk."""
+    import numpy as np
+    import torch
+
+    from oracle import forward as oforward
+    from oracle import ops as oops
+    from quail_amd import loop
+    from quail_amd.arena import KVArena
+    from quail_amd.model import SYNTHETIC_FALSE_IDS, SYNTHETIC_TRUE_IDS
+
+    torch.set_num_threads(threads)
+    w = oforward.cpu_weights(model)
+    gemm = oforward.DequantGemm()
+    for L in w["layers"]:
+        for name in ("qkv", "o", "gate_up", "down"):
+            q, s = L[name]
+            gemm.cache[q.data_ptr()] = oops.dequant_weight(q, s).T.contiguous()
+    kept = np.concatenate([anchor, frame])
+    rows = sum(-(-(len(kept) % 16 + len(p)) // 16) for p in partners)
+    pages = -(-len(kept) // 16) + rows + 4
+    arena = KVArena(1, pages, 16, 1, 1, device="cpu", allocate=False)
+    arena.activate(0, len(kept), capacity_tokens=len(kept))
+    group = dict(key=0, prefix=list(anchor), f=len(anchor), suffixes=[list(frame)],
+                 write_suffix_tokens=len(frame))
+    pairs = dict(key=0, prefix=None, f=len(kept), suffixes=[list(p) for p in partners])
+    chunk = loop.pack_chunk(torch, arena, [group, pairs], attention_mode="unified")
+    oarena = oforward.OracleArena(spec.layers, pages, spec.n_kv, spec.d_head)
+    t0 = time.perf_counter()
+    normed = oforward.forward_chunk(w, chunk.host, "unified", oarena, gemm=gemm)
+    bits, margins = oforward.readout(w, normed, SYNTHETIC_TRUE_IDS, SYNTHETIC_FALSE_IDS)
+    wall = time.perf_counter() - t0
+    for key in chunk.temporary_keys:
+        arena.free_key(key)
+    return dict(rows_per_s=len(partners) / wall, tok_per_s=chunk.tokens / wall, wall_s=wall,
+                tokens=chunk.tokens, bits=bits.tolist()[1:], margins=margins.tolist()[1:])
+
+
 def copy_calibration(nbytes):
     """A plain elementwise copy kernel that reads and writes `nbytes` each."""
     import torch
@@ -169,14 +215,22 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--workload", default="aiif-4b", choices=["aiif-4b", "aiif-32b"],
+    ap.add_argument("--workload", default="aiif-4b",
+                    choices=["aiif-4b", "aiif-32b", "join-4b"],
                     help="aiif-4b: Qwen3-4B, 64-token instruction, lognormal docs (median "
                          "180, cap 1024); aiif-32b: Qwen3-32B, 128-token instruction, docs "
-                         "uniform in [1024, 4096]")
+                         "uniform in [1024, 4096]; join-4b: Qwen3-4B AI join, anchors = "
+                         "48-token root + left doc (lognormal median 120), partners = right "
+                         "docs (lognormal median 120, cap 512), tree attention")
+    ap.add_argument("--anchors", type=int, default=32,
+                    help="join-4b: left rows (anchors); 256 is the full 256 x 256 join")
+    ap.add_argument("--partners", type=int, default=256, help="join-4b: right rows")
+    ap.add_argument("--cpu-pairs", type=int, default=4)
     ap.add_argument("--rows", type=int, default=None,
                     help="rows (default 4096 for aiif-4b, 256 for aiif-32b)")
     ap.add_argument("--layers", type=int, default=None)
-    ap.add_argument("--attention", default="unified", choices=["unified", "tree"])
+    ap.add_argument("--attention", default=None, choices=["unified", "tree"],
+                    help="default: unified for filters, tree for the join")
     ap.add_argument("--arena-pages", type=int, default=None)
     ap.add_argument("--cpu-rows", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -193,6 +247,12 @@ def main():
               f"multi-GPU path; rows shard per GPU with no device communication.",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "join-4b":
+        join_bench(args)
+        return
+    if args.attention is None:
+        args.attention = "unified"
 
     import torch
 
@@ -308,9 +368,105 @@ def main():
                       "frac_bf16_peak": round(k["attn_tflops"] / BF16_PEAK_TFLOPS, 4),
                       "gather_gbps": round(k["attn_gbps"], 1),
                       "gather_frac_hbm": round(k["attn_gbps"] / HBM_PEAK_GBPS, 4),
-                      "share_of_step": round(k["attn_ms"] / (ms_per_step * args.steps), 3)},
+                      "share_of_step": round(k["attn_ms"] / (ms_per_step * args.steps), 3),
+                      "calls": k["attn_kinds"]},
         "answers_true": int(sum(answers)), "deterministic_across_steps": steady,
         "build_s": round(build_s, 1),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def join_bench(args):
+    """The AI join workload: anchors x partners pairs, one TRUE/FALSE per pair."""
+    import torch
+
+    from quail_amd.aiif import JoinRunner, synthetic_join_workload
+    from quail_amd.model import build_random_qwen3
+    from quail_amd.specs import MI355X, QWEN3_4B_FP8
+    from dataclasses import replace
+
+    attention = args.attention or "tree"
+    spec = QWEN3_4B_FP8 if args.layers is None else replace(QWEN3_4B_FP8, layers=args.layers)
+    t_build = time.perf_counter()
+    model = build_random_qwen3(spec, seed=args.seed, device="cuda", max_pos=2048)
+    anchors, frame, partners = synthetic_join_workload(args.anchors, args.partners,
+                                                       seed=args.seed, vocab=spec.vocab)
+    clock = KernelClock(torch)
+    clock.n_q, clock.d, clock.n_kv = spec.n_q, spec.d_head, spec.n_kv
+    runner = JoinRunner(model, spec, device_spec=MI355X, n_pages=args.arena_pages,
+                        attention_mode=attention, gemm_hook=clock.gemm_hook,
+                        attention_hook=clock.attention_hook)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t_build
+    for _ in range(args.warmup):
+        runner.run_join(anchors, frame, partners)
+    clock.active = True
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    results = [runner.run_join(anchors, frame, partners) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    clock.active = False
+    k = clock.summary()
+    answers, stats = results[-1]
+    steady = all(r[0] == answers for r in results)
+    pairs = stats["rows"]
+    ms_per_step = wall / args.steps * 1e3
+    cpu = None
+    if not args.no_cpu_baseline and args.cpu_pairs > 0:
+        threads = min(16, len(os.sched_getaffinity(0)))
+        try:
+            base = cpu_baseline_join(model, spec, anchors[0], frame,
+                                     partners[:args.cpu_pairs], threads)
+            gpu_bits = answers[0][0][:args.cpu_pairs]
+            agree = sum(int(b == a) for b, a in zip(base["bits"], gpu_bits))
+            cpu = {"value": round(base["rows_per_s"], 4), "unit": "rows/s",
+                   "cores": threads, "kind": "port",
+                   "sample": (f"oracle forward (torch fp32, fp8 dequantized) of anchor 0 "
+                              f"(prefix + frame, once) and its first {args.cpu_pairs} "
+                              f"partners, unified attention: {base['tokens']} tokens, "
+                              f"{base['wall_s']:.1f} s; decisions agree with the GPU on "
+                              f"{agree}/{args.cpu_pairs} (margins "
+                              f"{[round(m, 3) for m in base['margins']]})")}
+        except Exception as exc:
+            cpu = {"value": None, "unit": "rows/s", "cores": 0, "kind": "port",
+                   "sample": f"failed: {exc!r}"}
+    line = {
+        "metric": "rows/s + prefill tok/s, Qwen3-4B fp8 AI join on 1 GPU (row = pair); "
+                  "attn/GEMM % of MFMA peak",
+        "value": round(pairs * args.steps / wall, 2), "unit": "rows/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 1),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8",
+        "data": "synthetic",
+        "config": {"workload": (f"AI join, Qwen3-4B-arch fp8 random init, {spec.layers} "
+                                f"layers, {args.anchors} x {args.partners} pairs, 48-token "
+                                f"root + left doc (lognormal median 120) anchors, 8-token "
+                                f"frame, partners = 4-token label + right doc (lognormal "
+                                f"median 120, cap 512) + 16-token tail, {attention} "
+                                f"attention"),
+                   "pairs": pairs, "anchors": args.anchors, "partners": args.partners,
+                   "layers": spec.layers, "fresh_tokens": stats["fresh_tokens"],
+                   "input_tokens": stats["input_tokens"], "chunks": stats.get("chunks"),
+                   "borrowed_tokens": stats.get("borrowed_tokens"),
+                   "chunk_budget": runner.budget, "arena_pages": runner.arena.n_pages},
+        "prefill_tok_per_s": round(stats["fresh_tokens"] * args.steps / wall, 1),
+        "input_tok_per_s": round(stats["input_tokens"] * args.steps / wall, 1),
+        "roofline": {"bound": "mfma", "achieved": round(k["gemm_tflops"], 1),
+                     "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(k["gemm_tflops"] / FP8_PEAK_TFLOPS, 4),
+                     "traffic": None, "traffic_source": "not measured for this workload",
+                     "algorithmic_bytes_per_launch": round(k["gemm_bytes"] / max(1, k["gemm_launches"])),
+                     "kernel": "qh fp8_gemm_kernel (all four projections)"},
+        "gemm": {"share_of_step": round(k["gemm_ms"] / (ms_per_step * args.steps), 3),
+                 "shapes": k["gemm_shapes"]},
+        "attention": {"tflops": round(k["attn_tflops"], 1),
+                      "frac_bf16_peak": round(k["attn_tflops"] / BF16_PEAK_TFLOPS, 4),
+                      "gather_gbps": round(k["attn_gbps"], 1),
+                      "share_of_step": round(k["attn_ms"] / (ms_per_step * args.steps), 3),
+                      "calls": k["attn_kinds"]},
+        "answers_true": int(sum(sum(row) for row in answers[0].values())),
+        "deterministic_across_steps": steady, "build_s": round(build_s, 1),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -119,3 +119,66 @@ class FilterRunner:
                      rows=len(docs), shared_tokens=tree.shared_tokens)
         self.last = stats
         return [answers[i][0] for i in range(len(docs))], stats
+
+
+def synthetic_join_workload(n_left, n_right, *, root_tokens=48, left_median=120,
+                            right_median=120, spread=230 / 180, left_cap=1024,
+                            right_cap=512, frame_tokens=8, label_tokens=4, tail_tokens=16,
+                            vocab=151_936, seed=0):
+    """Rows of an AI join over a Qwen3-sized vocabulary.
+
+    Anchor a = a shared `root_tokens`-token instruction + left document a
+    (written into the arena once; the prefix tree lets every anchor borrow
+    the root's whole pages). Each anchor's frame (`frame_tokens` ids, the
+    join framing the reference writes into the anchor's KV ahead of its
+    partners) follows it. Every partner suffix = a `label_tokens`-id
+    partner label + right document + a `tail_tokens`-id question tail, so
+    a pair's prompt is root + left doc + frame + label + right doc + tail
+    (the reference's render_join_prompt_ids layout, prompts.py). Document
+    lengths are rounded lognormals with the given medians and mean/median
+    ratio `spread`, capped. Returns (anchor prefixes, frame, partner suffixes).
+    """
+    rng = np.random.default_rng(seed)
+    root = rng.integers(0, vocab, size=root_tokens, dtype=np.int64)
+    left = lognormal_lengths(n_left, left_median, left_median * spread, left_cap, rng)
+    right = lognormal_lengths(n_right, right_median, right_median * spread, right_cap, rng)
+    anchors = [np.concatenate([root, rng.integers(0, vocab, size=int(n), dtype=np.int64)])
+               for n in left]
+    frame = rng.integers(0, vocab, size=frame_tokens, dtype=np.int64)
+    label = rng.integers(0, vocab, size=label_tokens, dtype=np.int64)
+    tail = rng.integers(0, vocab, size=tail_tokens, dtype=np.int64)
+    partners = [np.concatenate([label, rng.integers(0, vocab, size=int(n), dtype=np.int64),
+                                tail]) for n in right]
+    return anchors, frame, partners
+
+
+class JoinRunner(FilterRunner):
+    """One GPU's AI join executor (the join branch of backend.py:162-279):
+    the same model, arena, pipeline and readout as FilterRunner, driven by
+    loop.run_join over anchors with a prefix tree."""
+
+    def run_join(self, anchors, frame, partners, *, stages=1):
+        """Run the join; returns (answers[j][a] rows, stats)."""
+        torch = self.torch
+        tree = prefix_tree(anchors, budgets.PAGE_TOKENS)
+        self.answers.margins = []
+        stats = {}
+        frames = [list(frame)] * stages
+        suffixes = [[list(p) for p in partners]] * stages
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        answers, _, tokens = loop.run_join(
+            torch, self.arena, self.pipeline, self.answers, [list(a) for a in anchors],
+            suffixes, self.budget, stage_frames=frames,
+            attention_mode=self.attention_mode or "tree", prefix_tree=tree, stats=stats)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        if self.arena.accounting.owned:
+            raise AssertionError("the join left pages resident")
+        pairs = sum(len(row) for row in answers[-1].values())
+        input_tokens = sum((len(a) + len(frame)) * len(partners) + sum(map(len, partners))
+                           for a in anchors)
+        stats.update(wall_s=wall, fresh_tokens=tokens, input_tokens=input_tokens,
+                     rows=pairs, anchors=len(anchors), shared_tokens=tree.shared_tokens)
+        self.last = stats
+        return answers, stats

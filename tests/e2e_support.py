@@ -87,3 +87,32 @@ def tiny_workload(seed, n_rows, prefix=40, max_doc=150, tail_len=9, vocab=4096):
 def tiny_model(seed=0):
     return build_random_qwen3(TINY, seed=seed, device="cuda", max_pos=2048,
                               answer_token_ids=TINY_TRUE + TINY_FALSE)
+
+
+def gpu_join(model, spec, anchors, frame, partners, *, path, pages, budget, true_ids,
+             false_ids, stages=1):
+    """Run a join on the GPU; returns (answers, per-chunk margins of every
+    final row, records, stats)."""
+    arena = KVArena(len(model.model.layers), pages, 16, spec.n_kv, spec.d_head,
+                    dtype=torch.bfloat16, device="cuda")
+    pipe = Recorder(Qwen3Pipeline(model, arena, spec=spec))
+    rows = AnswerRows(torch, model, true_ids, false_ids)
+    ans = AsyncAnswers(torch, rows, keep_margins=True)
+    stats = {}
+    answers, _, _ = loop.run_join(
+        torch, arena, pipe, ans, [list(a) for a in anchors],
+        [[list(p) for p in partners]] * stages, budget, stage_frames=[list(frame)] * stages,
+        attention_mode=path, prefix_tree=prefix_tree(anchors, 16), stats=stats)
+    torch.cuda.synchronize()
+    assert not arena.accounting.owned
+    return answers, ans.margins, pipe.records, stats
+
+
+def tiny_join(seed, n_anchors, n_partners, root=40, max_doc=60, frame_len=5, vocab=4096):
+    rng = np.random.default_rng(seed)
+    head = rng.integers(0, vocab, size=root)
+    anchors = [np.concatenate([head, rng.integers(0, vocab, size=int(rng.integers(1, max_doc)))])
+               for _ in range(n_anchors)]
+    frame = rng.integers(0, vocab, size=frame_len)
+    partners = [rng.integers(0, vocab, size=int(rng.integers(2, 30))) for _ in range(n_partners)]
+    return anchors, frame, partners

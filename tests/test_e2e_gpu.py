@@ -251,3 +251,86 @@ def test_unified_and_tree_paths_agree_on_the_gpu():
     for d in range(len(docs)):
         if a[d] != b[d]:
             assert abs(ma[d]) <= 0.25 and abs(mb[d]) <= 0.25, f"row {d}"
+
+
+@pytest.mark.parametrize("path", ["unified", "tree"])
+def test_join_layers_match_the_oracle_teacher_forced(path):
+    """An AI join (anchors sharing a 40-token root, a frame entry, partner
+    streams cut across chunks; unified temporaries with kept-tail copies or
+    tree reads of the anchor) through 3 layers, teacher-forced against the
+    oracle replaying the same chunks, with the filter's bars."""
+    from e2e_support import tiny_join
+    spec = replace(TINY, layers=3)
+    model = build_random_qwen3(spec, seed=8, device="cuda", max_pos=2048,
+                               answer_token_ids=TINY_TRUE + TINY_FALSE)
+    anchors, frame, partners = tiny_join(seed=9, n_anchors=6, n_partners=13)
+    pages = 200
+    arena = KVArena(spec.layers, pages, 16, spec.n_kv, spec.d_head, device="cuda")
+    pipe = Qwen3Pipeline(model, arena, spec=spec)
+    traces, hosts = [], []
+
+    def trace(layer, hidden, residual):
+        traces[-1].append((hidden.float().cpu(),
+                           None if residual is None else residual.float().cpu()))
+
+    class Rec:
+        tree_attention, canvas_ids, needs_pages = True, (), False
+
+        def forward_chunk(self, chunk):
+            traces.append([])
+            hosts.append((chunk.host, chunk.attention_mode))
+            return pipe.forward_chunk(chunk)
+
+    pipe.trace = trace
+    ans = AsyncAnswers(torch, AnswerRows(torch, model, TINY_TRUE, TINY_FALSE))
+    stats = {}
+    out, _, _ = loop.run_join(torch, arena, Rec(), ans, [list(a) for a in anchors],
+                              [[list(p) for p in partners]], 300, stage_frames=[list(frame)],
+                              attention_mode=path, prefix_tree=prefix_tree(anchors, 16),
+                              stats=stats)
+    assert stats["chunks"] >= 3 and stats["borrowed_tokens"] > 0
+    assert sorted(out[0]) == list(range(len(anchors)))
+    assert all(len(row) == len(partners) for row in out[0].values())
+    if path == "unified":
+        assert any("tail_src" in host for host, _ in hosts)
+    else:
+        assert any("reads_rows" in host for host, _ in hosts)
+    w = oforward.cpu_weights(model)
+    oarena = oforward.OracleArena(spec.layers, pages, spec.n_kv, spec.d_head)
+    for (host, mode), layers in zip(hosts, traces):
+        for li, L in enumerate(w["layers"]):
+            h_in, r_in = layers[li]
+            h_in = h_in.to(torch.bfloat16)
+            r_in = None if r_in is None else r_in.to(torch.bfloat16)
+            h_ref, r_ref = oforward.layer_step(L, li, h_in, r_in, host, mode, oarena)
+            h_gpu, r_gpu = layers[li + 1]
+            worst = ((h_gpu - h_ref.float()).norm(dim=1)
+                     / h_ref.float().norm(dim=1).clamp(min=1e-6)).max().item()
+            rec = (li, _rel(h_gpu, h_ref), worst, _rel(r_gpu, r_ref))
+            assert rec[1] < 0.08 and rec[2] < 0.20 and rec[3] < 0.02, f"layer {rec}"
+
+
+@pytest.mark.parametrize("path", ["unified", "tree"])
+def test_join_decisions_agree_outside_the_noise_band(path):
+    """Every final row of every chunk of a 2-stage join (frame entries
+    included): GPU decisions against the oracle's replay, with the filter's
+    bars (disagreements only within 0.25 of a tie, >= 95% agreement)."""
+    from e2e_support import gpu_join, oracle_replay, tiny_join
+    model = build_random_qwen3(TINY, seed=10, device="cuda", max_pos=2048,
+                               answer_token_ids=TINY_TRUE + TINY_FALSE)
+    anchors, frame, partners = tiny_join(seed=11, n_anchors=8, n_partners=12)
+    pages = 300
+    _, margins, records, stats = gpu_join(model, TINY, anchors, frame, partners, path=path,
+                                          pages=pages, budget=400, true_ids=TINY_TRUE,
+                                          false_ids=TINY_FALSE, stages=2)
+    assert stats["chunks"] >= 3
+    ref = oracle_replay(model, TINY, records, pages, TINY_TRUE, TINY_FALSE)
+    agree = total = 0
+    for (_, _, normed), m_gpu, (_, bits, margin) in zip(records, margins, ref):
+        for g, r, mr in zip((m_gpu > 0).tolist(), bits.tolist(), margin.tolist()):
+            total += 1
+            agree += int(g) == r
+            if int(g) != r:
+                assert abs(mr) <= 0.25, f"decision differs at margin {mr:.4f}"
+    assert total >= 8 * 12 and agree >= 0.95 * total, f"{agree}/{total}"
+    print(f"join {path}: GPU-vs-oracle {agree}/{total} final rows")
