@@ -216,12 +216,14 @@ def main():
     ap.add_argument("--steps", type=int, default=2)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--workload", default="aiif-4b",
-                    choices=["aiif-4b", "aiif-32b", "join-4b"],
+                    choices=["aiif-4b", "aiif-32b", "join-4b", "attn-c1"],
                     help="aiif-4b: Qwen3-4B, 64-token instruction, lognormal docs (median "
                          "180, cap 1024); aiif-32b: Qwen3-32B, 128-token instruction, docs "
                          "uniform in [1024, 4096]; join-4b: Qwen3-4B AI join, anchors = "
                          "48-token root + left doc (lognormal median 120), partners = right "
-                         "docs (lognormal median 120, cap 512), tree attention")
+                         "docs (lognormal median 120, cap 512), tree attention; attn-c1: "
+                         "one attention layer, 64 rows sharing a 256-token prefix of a "
+                         "paged arena, suffixes U[32, 256], 32/8 heads")
     ap.add_argument("--anchors", type=int, default=32,
                     help="join-4b: left rows (anchors); 256 is the full 256 x 256 join")
     ap.add_argument("--partners", type=int, default=256, help="join-4b: right rows")
@@ -250,6 +252,9 @@ def main():
 
     if args.workload == "join-4b":
         join_bench(args)
+        return
+    if args.workload == "attn-c1":
+        attention_bench(args)
         return
     if args.attention is None:
         args.attention = "unified"
@@ -372,6 +377,156 @@ def main():
                       "calls": k["attn_kinds"]},
         "answers_true": int(sum(answers)), "deterministic_across_steps": steady,
         "build_s": round(build_s, 1),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def attention_bench(args):
+    """One prefix-shared attention layer (64 rows x 256-token prefix).
+
+    Inputs: Q, K, V ~ N(0, 1)/sqrt(128) bf16; the prefix's 16 pages and the
+    rows' own pages are a seeded random permutation of the arena's pages.
+    Timed per layer with HIP events on the launch stream:
+      unified   KV scatter of the rows into their pages + the paged causal
+                call (fp8 out) over prefix + own pages;
+      tree      the fused kernel: node (prefix pages) + own rows, one softmax;
+      two_pass  call A (own rows) + call B (node, stacked) + merge_attn_quant.
+    """
+    import numpy as np
+    import torch
+
+    from oracle import ops as oops
+    from quail_amd import kernels as K
+    from quail_amd import layout
+
+    rng = np.random.default_rng(args.seed)
+    n_q, n_kv, d, page, prefix, rows = 32, 8, 128, 16, 256, 64
+    suf = rng.integers(32, 257, size=rows)
+    T = int(suf.sum())
+    own_pages = [-(-int(n) // page) for n in suf]
+    n_pages = prefix // page + sum(own_pages) + 8
+    perm = rng.permutation(n_pages).astype(np.int32)
+    node_pages = perm[:prefix // page]
+    at = prefix // page
+    table_u = np.zeros((rows, (prefix + 256) // page), dtype=np.int32)
+    dst = []
+    for r, n in enumerate(suf):
+        mine = perm[at:at + own_pages[r]]
+        at += own_pages[r]
+        table_u[r, :prefix // page] = node_pages
+        table_u[r, prefix // page:prefix // page + own_pages[r]] = mine
+        j = np.arange(int(n))
+        dst.append(mine[j // page].astype(np.int64) * page + j % page)
+    dst = np.concatenate(dst)
+    cu = np.concatenate([[0], np.cumsum(suf)]).astype(np.int32)
+    g = torch.Generator().manual_seed(args.seed)
+    sd = 1 / np.sqrt(d)
+    q = (torch.randn(T, n_q, d, generator=g) * sd).to(torch.bfloat16)
+    k3 = (torch.randn(T, n_kv, d, generator=g) * sd).to(torch.bfloat16)
+    v3 = (torch.randn(T, n_kv, d, generator=g) * sd).to(torch.bfloat16)
+    k_rows = torch.zeros(n_pages * page, n_kv, d, dtype=torch.bfloat16)
+    v_rows = torch.zeros(n_pages * page, n_kv, d, dtype=torch.bfloat16)
+    node_rows = torch.from_numpy(node_pages[np.arange(prefix) // page].astype(np.int64) * page
+                                 + np.arange(prefix) % page)
+    k_rows[node_rows] = (torch.randn(prefix, n_kv, d, generator=g) * sd).to(torch.bfloat16)
+    v_rows[node_rows] = (torch.randn(prefix, n_kv, d, generator=g) * sd).to(torch.bfloat16)
+    dev = "cuda"
+    kp = layout.k_pool_from_rows(k_rows).to(dev)
+    vp = layout.v_pool_from_rows(v_rows).to(dev)
+    qd, kd, vd = q.to(dev), k3.to(dev), v3.to(dev)
+    cu_d = torch.from_numpy(cu).to(dev)
+    used_u = torch.from_numpy((prefix + suf).astype(np.int32)).to(dev)
+    tab_u = torch.from_numpy(table_u).to(dev)
+    src_d = torch.arange(T, dtype=torch.int64, device=dev)
+    dst_d = torch.from_numpy(dst).to(dev)
+    seg_read = torch.zeros(rows, dtype=torch.int32, device=dev)
+    node_tab = torch.from_numpy(node_pages[None, :].copy()).to(dev)
+    node_used = torch.tensor([prefix], dtype=torch.int32, device=dev)
+    scale = 1 / np.sqrt(d)
+    a_len = (cu_d[1:] - cu_d[:-1]).to(torch.int32)
+    all_rows = torch.arange(T, dtype=torch.int64, device=dev)
+    source = torch.arange(T, dtype=torch.int32, device=dev)
+    cu_b = torch.tensor([0, T], dtype=torch.int32, device=dev)
+
+    def unified():
+        K.kv_row_scatter(kd, vd, kp, vp, src_d, dst_d)
+        return K.attention_fp8(qd, cu_d, used_u, n_queries=T, max_q=int(suf.max()),
+                               softmax_scale=scale, causal=True, k_pool=kp, v_pool=vp,
+                               table=tab_u, n_kv=n_kv)
+
+    def tree():
+        return K.tree_attention(qd, kd, vd, cu_d, seg_read, softmax_scale=scale, k_pool=kp,
+                                v_pool=vp, table=node_tab, used=node_used)
+
+    def two_pass():
+        out_a, lse_a = K.attention(qd, cu_d, a_len, n_queries=T, max_q=int(suf.max()),
+                                   softmax_scale=scale, causal=True, k_rows=kd, v_rows=vd,
+                                   cu_k=cu_d, n_kv=n_kv, want_lse=True)
+        out_b, lse_b = K.attention(qd, cu_b, node_used, n_queries=T, max_q=T,
+                                   softmax_scale=scale, causal=False, k_pool=kp, v_pool=vp,
+                                   table=node_tab, q_rows=all_rows, n_kv=n_kv, want_lse=True)
+        return K.merge_attn_quant(out_a, lse_a, out_b, lse_b, source)
+
+    pairs = int((suf * prefix + suf * (suf + 1) // 2).sum())
+    flops = 4.0 * n_q * d * pairs
+    # unique HBM bytes: Q in (bf16), O out (e4m3 + scales), node K/V once,
+    # the rows' own K/V once
+    unique = T * n_q * d * 2 + T * n_q * (d + 4) + (prefix + T) * n_kv * d * 4
+    stream = torch.cuda.current_stream()
+    results = {}
+    iters = max(args.steps, 1) * 10
+    for name, fn in (("unified", unified), ("tree", tree), ("two_pass", two_pass)):
+        for _ in range(max(args.warmup, 1) * 3):
+            fn()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(iters):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / iters
+        results[name] = dict(us_per_layer=round(us, 2),
+                             tflops=round(flops / us / 1e6, 1),
+                             frac_bf16_peak=round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                             unique_gbps=round(unique / us / 1e3, 1))
+    # parity: the fused kernel (bf16 out) against the fp32 oracle, all rows
+    got = K.tree_attention(qd, kd, vd, cu_d, seg_read, softmax_scale=scale, k_pool=kp,
+                           v_pool=vp, table=node_tab, used=node_used, fp8=False).float().cpu()
+    cpu = None
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    t0 = time.perf_counter()
+    want = oops.tree_attention(q, k3, v3, cu, torch.zeros(rows, dtype=torch.int32), k_rows,
+                               v_rows, torch.from_numpy(node_pages[None, :].copy()),
+                               torch.tensor([prefix], dtype=torch.int32), scale)
+    cpu_s = time.perf_counter() - t0
+    err = (got - want).abs().max().item()
+    if not args.no_cpu_baseline:
+        cpu = {"value": round(flops / cpu_s / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+               "kind": "port",
+               "sample": (f"oracle tree attention (torch fp32) over the whole layer: "
+                          f"{cpu_s * 1e6:.0f} us per layer")}
+    best = results["tree"]
+    line = {
+        "metric": "prefix-shared attention TFLOP/s per layer (64 rows x 256-token prefix, "
+                  "32/8 heads, d 128) on 1 GPU; % of bf16 MFMA peak",
+        "value": best["tflops"], "unit": "TFLOP/s", "n_gpus": 1, "steps": iters,
+        "warmup": max(args.warmup, 1) * 3, "ms_per_step": round(best["us_per_layer"] / 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "one attention layer over a paged KV arena: 64 rows sharing a "
+                               "256-token prefix, suffixes U[32, 256], 32 q / 8 kv heads, "
+                               "head_dim 128, page 16, pages randomly permuted",
+                   "rows": rows, "query_rows": T, "pairs": pairs, "gflop": round(flops / 1e9, 2),
+                   "unique_bytes": unique},
+        "roofline": {"bound": "mfma", "achieved": best["tflops"], "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": best["frac_bf16_peak"], "traffic": None,
+                     "kernel": "qh attn_tree_kernel (fused node + own rows, fp8 out)"},
+        "paths": results,
+        "parity_max_abs_vs_oracle": round(err, 6),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -201,6 +201,30 @@ int qh_attention_fp8(const void* q, long ldq, int q_rows_total,
                      qh_stream_t stream);
 
 /*
+ * The tree path's whole attention in one pass: replaces Engine.
+ * attention_tree's call A (varlen causal over the chunk's own segments),
+ * call B (non-causal paged read of resident KV) and merge_attn_quant
+ * (attention.py:835-870, :738-759, :429-473). Row t of causal segment s
+ * (cu_a [n_seg + 1] over the chunk's rows; t counted from the segment
+ * start) attends the read_used[r] keys of page-table row r = seg_read[s]
+ * (none when r = -1) and its segment's own rows 0..t of k_rows / v_rows
+ * [n_rows, n_kv, 128] (row stride ld_kv elements), under one softmax:
+ * the exact attention that calls A and B + the LSE merge compose. Output
+ * as qh_attention (bf16 out, row stride ldo) or, with out_q non-NULL, as
+ * qh_attention_fp8 (e4m3 [n_rows, n_q*128] + scales [n_q, n_rows]).
+ * Workspace: qh_attention_workspace_bytes(n_seg).
+ */
+int qh_tree_attention(const void* q, long ldq, int n_rows, const void* k_rows,
+                      const void* v_rows, long ld_kv, const int32_t* cu_a,
+                      const int32_t* seg_read, int n_seg, const void* k_pool,
+                      const void* v_pool, int pool_pages, const int32_t* table,
+                      int table_width, const int32_t* read_used, int n_reads,
+                      int page_tokens, int n_q, int n_kv, int d,
+                      float softmax_scale, void* out, long ldo, void* out_q,
+                      long ld_out_q, float* scales, int ue8m0, void* workspace,
+                      size_t workspace_bytes, qh_stream_t stream);
+
+/*
  * LSE merge of the tree path's two attention calls fused with per-head fp8
  * quantization. Replaces Triton merge_attn_quant (attention.py:429-473,
  * :738-759): where source[t] >= 0, w = bf16(sigmoid(lse_b - lse_a)),

@@ -320,6 +320,37 @@ def varlen_attention(q3, k3, v3, cu, scale, causal=True):
     return out, lse
 
 
+def tree_attention(q3, k3, v3, cu_a, seg_read, k_pool, v_pool, table, used, scale,
+                   page=PAGE):
+    """The tree path's attention in exact arithmetic (attention.py:835-870).
+
+    Segment s of cu_a (rows a..b of the chunk) attends the used[r] keys of
+    page-table row r = seg_read[s] (when r >= 0) in full, and its own rows
+    k3/v3[a..b] causally; one softmax over both key sets. Call A (own
+    segments), call B (the read) and the LSE merge compute this same value
+    up to their intermediate bf16 roundings. Returns out fp32 [T, H, d].
+    """
+    cu = [int(x) for x in cu_a]
+    T, H, d = q3.shape
+    out = torch.zeros(T, H, d)
+    for s in range(len(cu) - 1):
+        a, b = cu[s], cu[s + 1]
+        c = b - a
+        if c == 0:
+            continue
+        r = int(seg_read[s])
+        own_vis = causal_visible(c, c)
+        if r >= 0:
+            n = int(used[r])
+            k = torch.cat([gather_pages(k_pool, table[r], n, page).float(), k3[a:b].float()])
+            v = torch.cat([gather_pages(v_pool, table[r], n, page).float(), v3[a:b].float()])
+            vis = torch.cat([torch.ones(c, n, dtype=torch.bool), own_vis], dim=1)
+        else:
+            k, v, vis = k3[a:b], v3[a:b], own_vis
+        out[a:b], _ = attend(q3[a:b], k, v, scale, vis)
+    return out
+
+
 def merge_attn(out_a, lse_a, out_b, lse_b, source):
     """The LSE merge of merge_attn_quant before its quant (attention.py:440-464).
 

@@ -16,6 +16,8 @@
 // V is transposed on its way into LDS).
 #include "common.h"
 
+#include <type_traits>
+
 namespace qh {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -620,6 +622,382 @@ __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Tree attention, fused (the tree path's call A + call B + merge in one pass).
+//
+// The chunk's rows form causal segments (cu_a). A segment may read a node:
+// resident arena pages every one of its rows attends in full (a parent's
+// shared prefix, or a kept anchor's document) - seg_read[s] names the read
+// sequence (page table row, used keys) or is -1. One workgroup = 32 rows of
+// one segment x the 4 query heads of one KV head; it walks the node's pages
+// (non-causal) and then the segment's own rows (causal) as one stream of
+// 32-key tiles with one online softmax, so no LSE, second output or merge
+// pass exists, and q-tiles of the rows under one node run back to back, so
+// the node's pages are fetched from HBM once and served from L2 after.
+//
+// Node tiles reach LDS exactly as in attn_paged_kernel (K and V^T page
+// blocks by DMA). Own tiles are the chunk's contiguous K/V rows
+// [T, n_kv, 128], also by DMA: K into the same swizzled [key][d] layout,
+// V into [key][d] rows whose 16-byte chunks are XOR-swizzled by 4 (key % 4);
+// the P.V operand (8 consecutive keys of one d per lane) is then read with
+// two ds_read_b64_tr_b16. Within a 16-lane group, that instruction hands
+// lane i element i % 4 of the 8-byte rows addressed by lanes i/4, 4 + i/4,
+// 8 + i/4 and 12 + i/4, so lane r addresses key kbase + r/4 at
+// d = dbase + 4 (r % 4) and lane i receives keys kbase .. kbase+3 of
+// d = dbase + i.
+struct TreeParams {
+  const uint16_t* q;
+  long ldq;
+  int n_rows;                 // T: chunk rows (q, k_rows, v_rows, outputs)
+  const uint16_t* k_rows;
+  const uint16_t* v_rows;
+  long ld_kv;                 // elements per row of k_rows / v_rows (n_kv * 128)
+  const int32_t* cu_a;        // [n_seg + 1]
+  const int32_t* seg_read;    // [n_seg]: read sequence or -1
+  int n_seg;
+  const uint16_t* k_pool;
+  const uint16_t* v_pool;
+  int pool_pages;
+  const int32_t* table;       // [n_reads, table_width]
+  int table_width;
+  const int32_t* read_used;   // [n_reads]
+  int n_reads;
+  int n_q;
+  int n_kv;
+  float scale_log2;
+  uint16_t* out;              // bf16 [T, n_q*128] (row stride ldo), or
+  long ldo;
+  uint8_t* out_q;             // e4m3 [T, n_q*128] + scales [n_q, T]
+  long ld_out_q;
+  float* out_scales;
+  int ue8m0;
+  const int32_t* tile_off;    // [n_seg + 1] exclusive scan of q-tiles
+};
+
+__device__ __forceinline__ int vswz(int key) { return 4 * (key & 3); }
+
+typedef short ts16x4 __attribute__((ext_vector_type(4)));
+
+template <bool FP8OUT>
+__global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
+  using namespace pattn;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int col = lane & 31;
+
+  // ---- segment and q-tile (heaviest q-tile of a segment first) -------------
+  const int b = blockIdx.x;
+  const int total_tiles = p.tile_off[p.n_seg];
+  if (b >= total_tiles) return;
+  int lo = 0, hi = p.n_seg - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (p.tile_off[mid] <= b) lo = mid; else hi = mid - 1;
+  }
+  const int s = lo;
+  const int q0 = p.cu_a[s];
+  const int count = p.cu_a[s + 1] - q0;
+  const int n_qt = (count + BQ - 1) / BQ;
+  const int i0 = (n_qt - 1 - (b - p.tile_off[s])) * BQ;
+  const int group = p.n_q / p.n_kv;
+  const int hq = blockIdx.y * HPW + wave;
+  const int hk = (blockIdx.y * HPW) / group;
+  int r = p.seg_read[s];
+  if (r >= p.n_reads) r = -1;
+  const int node_keys = r >= 0 ? max(0, p.read_used[r]) : 0;
+  const int n1 = (node_keys + BKV - 1) / BKV;          // node tiles
+  const int own_keys = min(count, i0 + BQ);            // causal: rows < i0 + 32
+  const int n_tiles = n1 + (own_keys + BKV - 1) / BKV;
+  const int my_i = i0 + col;
+
+  // ---- DMA roles: wave (region, pit) moves K (region 0) or V (region 1) of
+  // keys 16 pit .. 16 pit + 15 of a tile, as four 1 KiB pieces -------------
+  const int region = wave >> 1;
+  const int pit = wave & 1;
+  uint32_t voff_node[4], voff_own[4];
+  const uint32_t row_bytes = (uint32_t)p.ld_kv * 2u;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int P = 1024 * c + 16 * lane;  // byte position in the wave's 4 KiB block
+    const int r16 = P >> 8, pc = (P >> 4) & 15;
+    if (region == 0) {
+      voff_node[c] = (uint32_t)(r16 * 256 + ((pc ^ kswz(16 * pit + r16)) * 16));
+      voff_own[c] = (uint32_t)r16 * row_bytes + (uint32_t)hk * 256u +
+                    (uint32_t)((pc ^ kswz(16 * pit + r16)) * 16);
+    } else {
+      const int d = P >> 5, ph = (P >> 4) & 1;
+      voff_node[c] = (uint32_t)(d * 32 + ((ph ^ ((d >> 3) & 1)) * 16));
+      voff_own[c] = (uint32_t)r16 * row_bytes + (uint32_t)hk * 256u +
+                    (uint32_t)((pc ^ vswz(16 * pit + r16)) * 16);
+    }
+  }
+  const uint16_t* pool = region ? p.v_pool : p.k_pool;
+  const uint16_t* own_rows = region ? p.v_rows : p.k_rows;
+  const pi32x4 rtab = attn_rsrc(p.table, r >= 0 ? (uint32_t)p.n_reads * (uint32_t)p.table_width * 4u : 0u);
+  const long tab_row = (long)(r >= 0 ? r : 0) * p.table_width;
+  auto tab_off = [&](int t) __attribute__((always_inline)) {
+    const int pidx = min(2 * t + pit, p.table_width - 1);
+    return (uint32_t)((tab_row + max(pidx, 0)) * 4);
+  };
+  auto load_page_id = [&](int t, float& dst) __attribute__((always_inline)) {
+    asm volatile("buffer_load_dword %0, off, %1, %2"
+                 : "=v"(dst) : "s"(rtab), "s"(tab_off(t)) : "memory");
+  };
+  // this wave's four DMA pieces of tile t into stage t % NST
+  auto dma_tile = [&](int t, int page_id) __attribute__((always_inline)) {
+    const uint32_t base =
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(
+            lds + (t % NST) * STAGE + region * HALF + pit * 4096);
+    if (t < n1) {
+      const int pidx = 2 * t + pit;
+      const bool live = pidx < p.table_width && pidx * PAGE < node_keys && page_id >= 0 &&
+                        page_id < p.pool_pages;
+      const int slots = live ? min(PAGE, node_keys - pidx * PAGE) : 0;
+      const uint32_t bytes = region ? (live ? 4096u : 0u) : (uint32_t)slots * 256u;
+      const uint16_t* blk = pool + ((long)(live ? page_id : 0) * p.n_kv + hk) * (PAGE * D);
+      const pi32x4 rs = attn_rsrc(blk, bytes);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        asm volatile(
+            "s_mov_b32 m0, %0\n\t"
+            "buffer_load_dwordx4 %1, %2, 0 offen lds"
+            :
+            : "s"(base + 1024 * c), "v"(voff_node[c]), "s"(rs)
+            : "memory", "m0");
+    } else {
+      // own keys 32 (t - n1) + 16 pit + 0..15: chunk rows q0 + those keys;
+      // rows past the chunk (or past the tiles) read zero
+      const long row0 = (long)q0 + 32L * (t - n1) + 16 * pit;
+      const bool live = t < n_tiles && row0 < p.n_rows;
+      const long rows_left = live ? (long)p.n_rows - row0 : 0;
+      const pi32x4 rs = attn_rsrc(own_rows + (live ? row0 : 0) * p.ld_kv,
+                                  (uint32_t)(rows_left * (long)row_bytes));
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        asm volatile(
+            "s_mov_b32 m0, %0\n\t"
+            "buffer_load_dwordx4 %1, %2, 0 offen lds"
+            :
+            : "s"(base + 1024 * c), "v"(voff_own[c]), "s"(rs)
+            : "memory", "m0");
+    }
+  };
+
+  // ---- Q fragments: lane holds Q[query col][16*st + 8*half .. +7] -----------
+  typedef int qi32x4 __attribute__((ext_vector_type(4)));
+  qi32x4 qraw[8];
+  {
+    const long row = (long)q0 + my_i;
+    const bool ok = my_i < count && row < p.n_rows;
+    const uint32_t qoff = ok ? (uint32_t)(row * p.ldq * 2 + (long)hq * D * 2 + 16 * half)
+                             : 0x80000000u;
+    const pi32x4 rq = attn_rsrc(p.q, (uint32_t)((long)p.n_rows * p.ldq * 2));
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+      asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3"
+                   : "=v"(qraw[st]) : "v"(qoff), "s"(rq), "i"(32 * st) : "memory");
+  }
+
+  // ---- prologue: page ids of node tiles 0..2 (scalar), DMA of tiles 0, 1 -----
+  auto page_of = [&](int t) __attribute__((always_inline)) {
+    return (r >= 0 && t < n1) ? p.table[tab_row + min(2 * t + pit, p.table_width - 1)] : -1;
+  };
+  const int pg0 = page_of(0), pg1 = page_of(1), pg2 = page_of(2);
+  dma_tile(0, pg0);
+  dma_tile(1, pg1);
+  asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // Q and tile 0 landed
+  asm volatile("" : "+v"(qraw[0]), "+v"(qraw[1]), "+v"(qraw[2]), "+v"(qraw[3]),
+               "+v"(qraw[4]), "+v"(qraw[5]), "+v"(qraw[6]), "+v"(qraw[7]));
+  bf16x8_t qf[8];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) qf[st] = __builtin_bit_cast(bf16x8_t, qraw[st]);
+
+  f32x16 acc_o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int a = 0; a < 16; ++a) acc_o[db][a] = 0.f;
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  float pg_next = __builtin_bit_cast(float, pg2);
+
+  // own-tile P.V operand addresses (see the note above the kernel): lane
+  // group G = lane / 16 covers d = 32 db + 16 (G % 2) + lane % 16 and keys
+  // 16 pt + 8 (G / 2) + 4 u + 0..3; lane addresses key + (lane % 16) / 4
+  const int gi = lane & 15;
+  const int tr_key = 8 * (lane >> 5) + (gi >> 2);
+  const int tr_chunk = 2 * ((lane >> 4) & 1) + ((gi & 3) >> 1);
+  const int tr_byte = (gi & 1) * 8;
+
+  const int kq = kperm(col);
+  // one 32-key tile; NODE is the phase (the two phases' P.V operands differ)
+  auto tile = [&](int t, auto node_c) __attribute__((always_inline)) {
+    constexpr bool node = decltype(node_c)::value;
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    asm volatile("" : "+v"(pg_next));
+    const int page_t2 = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, pg_next));
+    __syncthreads();  // stage t visible to all; stage t-1 free
+    load_page_id(t + 3, pg_next);
+    dma_tile(t + 2, page_t2);
+
+    uint8_t* st_base = lds + (t % NST) * STAGE;
+    const int key0 = node ? t * BKV : (t - n1) * BKV;
+    // a partial last node page: zero its V^T slots past node_keys
+    if (node && key0 + BKV > node_keys && ((node_keys & (PAGE - 1)) != 0)) {
+      const int zpit = (node_keys - key0) >> 4;
+      const int valid = node_keys & (PAGE - 1);
+      if (zpit < 2) {
+        const int d = tid >> 1, ph = tid & 1;
+        const int lh = ph ^ ((d >> 3) & 1);
+        uint16_t* vp = reinterpret_cast<uint16_t*>(st_base + HALF + zpit * 4096 + d * 32 + ph * 16);
+        bf16x8 v = load8(vp);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (8 * lh + e >= valid) v.set(e, 0);
+        store8(vp, v);
+      }
+      __syncthreads();
+    }
+
+    // ---- S^T = K Q^T ---------------------------------------------------------
+    f32x16 sacc;
+#pragma unroll
+    for (int a = 0; a < 16; ++a) sacc[a] = 0.f;
+    const uint8_t* krow = st_base + kq * 256;
+    const int ksw = kswz(kq);
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const bf16x8_t af =
+          *reinterpret_cast<const bf16x8_t*>(krow + (((2 * st + half) ^ ksw) * 16));
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[st], sacc, 0, 0, 0);
+    }
+    // ---- mask, scale, online softmax (log2 domain) -------------------------
+    const int lim = node ? node_keys : my_i + 1;
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int a = 0; a < 16; ++a) {
+      const int key = key0 + kperm(8 * (a >> 2) + 4 * half + (a & 3));
+      const float v = key < lim ? sacc[a] * p.scale_log2 : -INFINITY;
+      sacc[a] = v;
+      tmax = fmaxf(tmax, v);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+    float psum = 0.f;
+#pragma unroll
+    for (int a = 0; a < 16; ++a) {
+      const float e = (m_new == -INFINITY) ? 0.f : exp2f(sacc[a] - m_new);
+      sacc[a] = e;
+      psum += e;
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int a = 0; a < 16; ++a) acc_o[db][a] *= alpha;
+
+    // ---- O^T += V^T P^T over the tile's two 16-key steps ---------------------
+#pragma unroll
+    for (int pt = 0; pt < 2; ++pt) {
+      bf16x8_t pf;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pf[e] = (__bf16)sacc[8 * pt + e];
+      if constexpr (node) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const int d = 32 * db + col;
+          const bf16x8_t vf = *reinterpret_cast<const bf16x8_t*>(
+              st_base + HALF + pt * 4096 + d * 32 + ((half ^ ((d >> 3) & 1)) * 16));
+          acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc_o[db], 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          ts16x4 part[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int key = 16 * pt + 4 * u + tr_key;
+            const int chunk = (4 * db + tr_chunk) ^ vswz(key);
+            auto a = (__attribute__((address_space(3))) ts16x4*)(
+                (__attribute__((address_space(3))) uint8_t*)(
+                    (const __attribute__((address_space(3))) void*)(st_base + HALF)) +
+                key * 256 + chunk * 16 + tr_byte);
+            part[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(a);
+          }
+          const ts16x4 x0 = part[0], x1 = part[1];
+          typedef short ts16x8 __attribute__((ext_vector_type(8)));
+          const ts16x8 both = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+          const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, both);
+          acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc_o[db], 0, 0, 0);
+          // 16 wait states before anything may reuse vf's registers: without
+          // them the next ds_read_b64_tr_b16 refilling these registers
+          // corrupted this MFMA's A operand (wrong, run-to-run varying
+          // results on gfx950; the ds_read_b128 fragments of the node path
+          // never showed it). The padding sits inside the MFMA's own
+          // 32-cycle issue window.
+          __builtin_amdgcn_sched_barrier(0);
+          asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+  };
+  for (int t = 0; t < n1; ++t) tile(t, std::true_type{});
+  for (int t = n1; t < n_tiles; ++t) tile(t, std::false_type{});
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outlives the workgroup
+
+  // ---- epilogue -------------------------------------------------------------
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  const long qi = q0 + my_i;
+  if constexpr (FP8OUT) {
+    float amax = 0.f;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int a = 0; a < 16; ++a) {
+        const float v = round_bf16(acc_o[db][a] * inv);
+        acc_o[db][a] = v;
+        amax = fmaxf(amax, fabsf(v));
+      }
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    if (my_i >= count) return;
+    const float scale = group_scale(amax, p.ue8m0 != 0);
+    uint8_t* qp = p.out_q + qi * p.ld_out_q + (long)hq * D;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) w |= quant_e4m3(acc_o[db][4 * g + rr], scale) << (8 * rr);
+        *reinterpret_cast<uint32_t*>(qp + 32 * db + 8 * g + 4 * half) = w;
+      }
+    if (half == 0) p.out_scales[(long)hq * p.n_rows + qi] = scale;
+  } else {
+    if (my_i >= count) return;
+    uint16_t* op = p.out + qi * p.ldo + (long)hq * D;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * db + 8 * g + 4 * half;
+        uint32_t w0 = f32_to_bf16(acc_o[db][4 * g + 0] * inv) |
+                      (f32_to_bf16(acc_o[db][4 * g + 1] * inv) << 16);
+        uint32_t w1 = f32_to_bf16(acc_o[db][4 * g + 2] * inv) |
+                      (f32_to_bf16(acc_o[db][4 * g + 3] * inv) << 16);
+        *reinterpret_cast<uint2*>(op + d) = make_uint2(w0, w1);
+      }
+  }
+}
+
 }  // namespace qh
 
 using namespace qh;
@@ -755,4 +1133,82 @@ extern "C" int qh_attention_fp8(const void* q, long ldq, int q_rows_total,
                           n_seqs, n_queries, max_q, n_q, n_kv, d, softmax_scale, causal,
                           nullptr, 0, nullptr, 0, out_q, ld_out_q, scales, ue8m0, workspace,
                           workspace_bytes, stream);
+}
+
+extern "C" int qh_tree_attention(const void* q, long ldq, int n_rows, const void* k_rows,
+                                 const void* v_rows, long ld_kv, const int32_t* cu_a,
+                                 const int32_t* seg_read, int n_seg, const void* k_pool,
+                                 const void* v_pool, int pool_pages, const int32_t* table,
+                                 int table_width, const int32_t* read_used, int n_reads,
+                                 int page_tokens, int n_q, int n_kv, int d,
+                                 float softmax_scale, void* out, long ldo, void* out_q,
+                                 long ld_out_q, float* scales, int ue8m0, void* workspace,
+                                 size_t workspace_bytes, qh_stream_t stream) {
+  QH_REQUIRE(d == attn::D, "tree_attention: head_dim %d unsupported (128 only)", d);
+  QH_REQUIRE(n_q > 0 && n_kv > 0 && n_q % n_kv == 0 && (n_q / n_kv) % attn::HPW == 0,
+             "tree_attention: n_q=%d n_kv=%d needs a GQA group that is a multiple of 4",
+             n_q, n_kv);
+  QH_REQUIRE(n_rows >= 0 && n_seg >= 0 && n_reads >= 0, "tree_attention: negative sizes");
+  if (n_rows == 0 || n_seg == 0) return QH_OK;
+  const bool fp8 = out_q != nullptr;
+  QH_REQUIRE(q && k_rows && v_rows && cu_a && seg_read && (fp8 ? scales != nullptr : out != nullptr),
+             "tree_attention: null pointer");
+  QH_REQUIRE(ldq >= (long)n_q * d && ldq % 8 == 0, "tree_attention: row stride ldq=%ld", ldq);
+  QH_REQUIRE(ld_kv >= (long)n_kv * d && ld_kv % 8 == 0, "tree_attention: row stride ld_kv=%ld",
+             ld_kv);
+  if (fp8)
+    QH_REQUIRE(ld_out_q >= (long)n_q * d && ld_out_q % 16 == 0,
+               "tree_attention: fp8 row stride %ld", ld_out_q);
+  else
+    QH_REQUIRE(ldo >= (long)n_q * d && ldo % 8 == 0, "tree_attention: row stride ldo=%ld", ldo);
+  if (n_reads > 0)
+    QH_REQUIRE(k_pool && v_pool && pool_pages > 0 && table && table_width > 0 && read_used,
+               "tree_attention: reads without pools, table or used");
+  QH_REQUIRE(page_tokens == attn::PAGE, "tree_attention: page_tokens %d unsupported (16 only)",
+             page_tokens);
+  // the kernel addresses q, the rows and the table through 32-bit buffer offsets
+  QH_REQUIRE((long)n_rows * ldq * 2 < 0x80000000L && (long)n_rows * ld_kv * 2 < 0x80000000L &&
+                 (long)n_reads * table_width * 4 < 0x80000000L,
+             "tree_attention: q, k/v rows or page table exceed 2 GiB");
+  QH_REQUIRE(workspace && workspace_bytes >= qh_attention_workspace_bytes(n_seg),
+             "tree_attention: workspace of %zu bytes needed", qh_attention_workspace_bytes(n_seg));
+  QH_REQUIRE(((uintptr_t)workspace & 15) == 0, "tree_attention: workspace must be 16-byte aligned");
+  int32_t* tile_off = (int32_t*)workspace;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(attn_tile_scan_kernel, dim3(1), dim3(1024), 0, st, cu_a, n_seg, tile_off);
+  int rc = launch_status("tree attention tile scan");
+  if (rc) return rc;
+  TreeParams p;
+  p.q = (const uint16_t*)q;
+  p.ldq = ldq;
+  p.n_rows = n_rows;
+  p.k_rows = (const uint16_t*)k_rows;
+  p.v_rows = (const uint16_t*)v_rows;
+  p.ld_kv = ld_kv;
+  p.cu_a = cu_a;
+  p.seg_read = seg_read;
+  p.n_seg = n_seg;
+  p.k_pool = (const uint16_t*)k_pool;
+  p.v_pool = (const uint16_t*)v_pool;
+  p.pool_pages = pool_pages;
+  p.table = table;
+  p.table_width = table_width;
+  p.read_used = read_used;
+  p.n_reads = n_reads;
+  p.n_q = n_q;
+  p.n_kv = n_kv;
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  p.out = (uint16_t*)out;
+  p.ldo = ldo;
+  p.out_q = (uint8_t*)out_q;
+  p.ld_out_q = ld_out_q;
+  p.out_scales = scales;
+  p.ue8m0 = ue8m0;
+  p.tile_off = tile_off;
+  // upper bound on the q-tiles: sum ceil(c/32) <= n_rows/32 + n_seg
+  const long max_tiles = (long)n_rows / attn::BQ + n_seg;
+  dim3 grid((unsigned)max_tiles, (unsigned)(n_q / attn::HPW));
+  if (fp8) hipLaunchKernelGGL((attn_tree_kernel<true>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((attn_tree_kernel<false>), grid, dim3(256), 0, st, p);
+  return launch_status("tree attention");
 }

@@ -9,10 +9,13 @@ libquail_hip.so; nothing falls back to torch math. Two attention paths:
            kept-page tail copies of suffix temporaries), then one paged
            causal call in which every row reads the KV its document needs
            (attention.py:878-953); output quantized per 1x128 group.
-  tree     scatter the kept rows; call A: causal over the chunk's own
-           segments (chunk rows); call B: the readers of resident KV read it
-           stacked, non-causal; fused LSE merge + fp8 quant
-           (attention.py:835-870).
+  tree     scatter the kept rows, then one fused kernel: each causal
+           segment attends its node (resident KV its rows read, non-causal)
+           and its own rows (causal) under one softmax, fp8-quantized in the
+           epilogue - the exact attention the reference's call A + call B +
+           LSE merge compose (attention.py:835-870). tree_kernel="two_pass"
+           runs that three-launch form instead (call A, call B stacked,
+           merge_attn_quant), with the reference's bf16 roundings.
 """
 
 import math
@@ -41,8 +44,11 @@ class Engine:
 
     def __init__(self, arena, *, n_q, n_kv, head_dim, rotary, fp8=True,
                  kernels_name="quail", ue8m0=False, gemm_hook=None,
-                 attention_hook=None):
+                 attention_hook=None, tree_kernel="fused"):
         import torch
+        if tree_kernel not in ("fused", "two_pass"):
+            raise ValueError(f"tree_kernel must be 'fused' or 'two_pass', got {tree_kernel!r}")
+        self.tree_kernel = tree_kernel
         if not fp8:
             raise ValueError("this build runs fp8 block-scaled linears only")
         if kernels_name != "quail":
@@ -162,6 +168,18 @@ class Engine:
         if meta["kv_src"] is not None:
             kernels.kv_row_scatter(k3, v3, k_pool, v_pool, meta["kv_src"], meta["kv_dst"])
         reads = meta["reads"]
+        if self.tree_kernel == "fused":
+            work = meta.get("work", {})
+            pairs = work.get("own_pairs", 0) + work.get("read_pairs", 0)
+            kv_rows = n + work.get("read_kv_rows", 0)
+            q_out = self._timed("tree", pairs, kv_rows, n, lambda: kernels.tree_attention(
+                q3, k3, v3, meta["cu_a"], meta["a_read"], softmax_scale=self.softmax_scale,
+                k_pool=k_pool if reads is not None else None,
+                v_pool=v_pool if reads is not None else None,
+                table=reads["table"] if reads is not None else None,
+                used=reads["used"] if reads is not None else None, ue8m0=self.use_ue8m0))
+            meta["layer"] += 1
+            return q_out
         out_a, lse_a = self._causal_own(q3, k3, v3, meta, n, want_lse=reads is not None)
         if reads is None:
             meta["layer"] += 1

@@ -227,6 +227,51 @@ def attention_fp8(q3, cu_q, kv_len, *, n_queries, max_q, softmax_scale, causal,
     return q, scales
 
 
+def tree_attention(q3, k_rows, v_rows, cu_a, seg_read, *, softmax_scale, k_pool=None,
+                   v_pool=None, table=None, used=None, fp8=True, ue8m0=False):
+    """The tree path's attention in one kernel: each causal segment of cu_a
+    attends its read sequence seg_read[s] (page-table row of `table`, used
+    keys) in full and its own rows causally, under one softmax (the exact
+    result of attention.py:835-870's call A + call B + merge).
+
+    Returns (e4m3 [T, n_q*d], scales (T, n_q) column-major) with fp8, else
+    bf16 [T, n_q, d].
+    """
+    _check(q3, torch.bfloat16, "q", dim=3)
+    _check(k_rows, torch.bfloat16, "k_rows", dim=3)
+    _check(v_rows, torch.bfloat16, "v_rows", dim=3)
+    T, n_q, d = q3.shape
+    n_kv = k_rows.shape[1]
+    if k_rows.shape[0] != T or v_rows.shape != k_rows.shape or k_rows.stride(0) != v_rows.stride(0):
+        raise ValueError("k_rows / v_rows must be [T, n_kv, d] with one row stride")
+    if k_rows.stride(1) != d or q3.stride(1) != d:
+        raise ValueError("heads of q / k_rows / v_rows must be contiguous")
+    n_seg = cu_a.numel() - 1
+    if seg_read.dtype != torch.int32 or seg_read.numel() != n_seg:
+        raise ValueError("seg_read must be int32 with one entry per segment")
+    dev = q3.device
+    n_reads = 0 if table is None else table.shape[0]
+    if n_reads and (used is None or used.numel() != n_reads):
+        raise ValueError("used must have one entry per page-table row")
+    ws = torch.empty(_hip.workspace_bytes(n_seg), dtype=torch.uint8, device=dev)
+    out = q = scales = None
+    if fp8:
+        if d != GROUP:
+            raise ValueError("one quant group per head needs head_dim 128")
+        q = torch.empty((T, n_q * d), dtype=torch.float8_e4m3fn, device=dev)
+        scales = col_major_scales(T, n_q * d, dev)
+    else:
+        out = torch.empty((T, n_q, d), dtype=torch.bfloat16, device=dev)
+    _hip.call("qh_tree_attention", _ptr(q3), q3.stride(0), T, _ptr(k_rows), _ptr(v_rows),
+              k_rows.stride(0), _ptr(cu_a), _ptr(seg_read), n_seg,
+              _ptr(k_pool), _ptr(v_pool), 0 if k_pool is None else k_pool.shape[0],
+              _ptr(table), 0 if table is None else table.shape[1], _ptr(used), n_reads,
+              PAGE_TOKENS, n_q, n_kv, d, float(softmax_scale), _ptr(out),
+              0 if out is None else out.stride(0), _ptr(q), 0 if q is None else q.stride(0),
+              _ptr(scales), int(bool(ue8m0)), _ptr(ws), ws.numel(), _stream())
+    return (q, scales) if fp8 else out
+
+
 def merge_attn_quant(out_a, lse_a, out_b, lse_b, source, ue8m0=False):
     """LSE merge of the tree path + per-head fp8 quant (attention.py:429-473).
 

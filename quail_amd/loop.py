@@ -249,6 +249,10 @@ def pack_chunk(torch, arena, groups, timing=None, pinned=True, *, attention_mode
                       reads_table=table, reads_source=source)
         host_ints["reads"] = dict(max_q=max_q, max_used=max(read_used),
                                   n_rows=int(rows.size))
+    if tree_path:
+        # per causal segment, the read sequence all of its rows attend (or
+        # -1): what lets one fused kernel run call A, call B and the merge
+        arrays["a_read"] = _segment_reads(np.asarray(cu_a, dtype=np.int64), arrays)
     t = _tick(timing, "pack_reads", t)
 
     temporary_keys = []
@@ -364,6 +368,7 @@ def pack_chunk(torch, arena, groups, timing=None, pinned=True, *, attention_mode
         work["read_pairs"] = int((c * used).sum())
         work["read_kv_rows"] = int(used.sum())
     meta = dict(layer=0, kv_src=staged.get("kv_src"), kv_dst=staged.get("kv_dst"),
+                a_read=staged.get("a_read"),
                 work=work,
                 reads=reads, unified=unified, canvas=None, cu_a=staged["cu_a"],
                 a_len=staged["a_len"],
@@ -375,6 +380,30 @@ def pack_chunk(torch, arena, groups, timing=None, pinned=True, *, attention_mode
                   host=arrays)
     _tick(timing, "pack_h2d", t)
     return chunk
+
+
+def _segment_reads(cu_a, arrays):
+    """Read sequence of each causal segment, -1 for none.
+
+    Every reader range pack_chunk lays out covers whole segments (a stacked
+    group is one segment; a borrowing prefix is one; a group's suffixes all
+    read its key), so a segment's first row names the read of every row in
+    it; the check below holds that invariant.
+    """
+    n_seg = cu_a.size - 1
+    out = np.full(n_seg, -1, dtype=np.int32)
+    if "reads_source" not in arrays or n_seg == 0:
+        return out
+    source = arrays["reads_source"].astype(np.int64)
+    cu_q = arrays["reads_cu_q"].astype(np.int64)
+    row_read = np.where(source >= 0, np.searchsorted(cu_q, source, side="right") - 1, -1)
+    lens = np.diff(cu_a)
+    starts = cu_a[:-1]
+    nonempty = lens > 0
+    out[nonempty] = row_read[starts[nonempty]]
+    if row_read.size and not np.array_equal(row_read, np.repeat(out, lens)):
+        raise AssertionError("a causal segment mixes rows with different reads")
+    return out
 
 
 def attention_path(pipeline, requested, default="unified") -> str:

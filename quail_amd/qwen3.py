@@ -32,7 +32,8 @@ class Qwen3Pipeline(ModelPipeline):
     """Forward passes for a Qwen3-architecture fp8 model."""
 
     def __init__(self, model, arena, *, spec=None, kernels_name="quail",
-                 engine_class=Engine, ue8m0=False, gemm_hook=None, attention_hook=None):
+                 engine_class=Engine, ue8m0=False, gemm_hook=None, attention_hook=None,
+                 tree_kernel="fused"):
         import torch
         self.layers = model.model.layers
         self.embed = model.model.embed_tokens
@@ -42,7 +43,8 @@ class Qwen3Pipeline(ModelPipeline):
         self.engine = engine_class(arena, n_q=attn.num_heads, n_kv=attn.num_kv_heads,
                                    head_dim=attn.head_dim, rotary=attn.rotary_emb,
                                    fp8=fp8, kernels_name=kernels_name, ue8m0=ue8m0,
-                                   gemm_hook=gemm_hook, attention_hook=attention_hook)
+                                   gemm_hook=gemm_hook, attention_hook=attention_hook,
+                                   tree_kernel=tree_kernel)
         self.tree_attention = fp8
         widest = max(max(layer.self_attn.qkv_proj.weight.shape[0],
                          layer.mlp.gate_up_proj.weight.shape[0]) for layer in self.layers)

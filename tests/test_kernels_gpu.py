@@ -420,3 +420,184 @@ def test_gather_final_norm_and_answer_bits():
     clear = margin_ref.abs() > 0.05
     assert torch.equal(bits.cpu()[clear], bits_ref[clear])
     assert (margin.cpu() - margin_ref).abs().max().item() < 0.1
+
+
+def _tree_case(seed, *, n_nodes=3, segs=9, n_q=32, n_kv=8, d=128, nan_unread=True, sd=None):
+    """Chunk rows in causal segments; some segments read one of n_nodes
+    resident nodes (random lengths, partial last pages, permuted physical
+    pages); every arena row no node reads is NaN. Q, K, V ~ N(0, sd^2),
+    sd = 1/sqrt(d) by default (the C1 distribution)."""
+    sd = 1 / math.sqrt(d) if sd is None else sd
+    g = _gen(seed)
+    page = 16
+    node_len = [int(x) for x in torch.randint(1, 300, (n_nodes,), generator=g)]
+    widths = [-(-n // page) for n in node_len]
+    n_pages = sum(widths) + 5
+    perm = torch.randperm(n_pages, generator=g).to(torch.int32)
+    table = torch.zeros(n_nodes, max(widths), dtype=torch.int32)
+    at = 0
+    for i, w in enumerate(widths):
+        table[i, :w] = perm[at:at + w]
+        at += w
+    lens = [int(x) for x in torch.randint(1, 140, (segs,), generator=g)]
+    lens[0] = 1
+    cu_a = [0]
+    for n in lens:
+        cu_a.append(cu_a[-1] + n)
+    seg_read = torch.tensor([int(torch.randint(-1, n_nodes, (1,), generator=g)) for _ in lens],
+                            dtype=torch.int32)
+    T = cu_a[-1]
+    q = (torch.randn(T, n_q, d, generator=g) * sd).to(torch.bfloat16)
+    k3 = (torch.randn(T, n_kv, d, generator=g) * sd).to(torch.bfloat16)
+    v3 = (torch.randn(T, n_kv, d, generator=g) * sd).to(torch.bfloat16)
+    k_rows = (torch.randn(n_pages * page, n_kv, d, generator=g) * sd).to(torch.bfloat16)
+    v_rows = (torch.randn(n_pages * page, n_kv, d, generator=g) * sd).to(torch.bfloat16)
+    if nan_unread:
+        read = torch.zeros(n_pages * page, dtype=torch.bool)
+        for i, n in enumerate(node_len):
+            for j in range(n):
+                read[int(table[i, j // page]) * page + j % page] = True
+        k_rows[~read] = float("nan")
+        v_rows[~read] = float("nan")
+    return dict(q=q, k3=k3, v3=v3, k_rows=k_rows, v_rows=v_rows, table=table,
+                used=torch.tensor(node_len, dtype=torch.int32), cu_a=torch.tensor(cu_a, dtype=torch.int32),
+                seg_read=seg_read, T=T)
+
+
+def _run_tree(case, fp8, ue8m0=False):
+    kp = layout.k_pool_from_rows(case["k_rows"]).to(DEV)
+    vp = layout.v_pool_from_rows(case["v_rows"]).to(DEV)
+    return K.tree_attention(case["q"].to(DEV), case["k3"].to(DEV), case["v3"].to(DEV),
+                            case["cu_a"].to(DEV), case["seg_read"].to(DEV),
+                            softmax_scale=1 / math.sqrt(128), k_pool=kp, v_pool=vp,
+                            table=case["table"].to(DEV), used=case["used"].to(DEV), fp8=fp8,
+                            ue8m0=ue8m0)
+
+
+@pytest.mark.parametrize("seed,n_kv", [(60, 8), (61, 8), (62, 4)])
+def test_tree_attention_matches_the_oracle(seed, n_kv):
+    """The fused tree kernel (node pages, then own rows, one softmax) within
+    max-abs 2e-3 of the fp32 oracle; unread arena rows are NaN."""
+    case = _tree_case(seed, n_kv=n_kv)
+    got = _run_tree(case, fp8=False).float().cpu()
+    want = ref.tree_attention(case["q"], case["k3"], case["v3"], case["cu_a"], case["seg_read"],
+                              case["k_rows"], case["v_rows"], case["table"], case["used"],
+                              1 / math.sqrt(128))
+    assert torch.isfinite(got).all()
+    err = (got - want).abs().max().item()
+    assert err <= 2e-3, f"max-abs {err}"
+
+
+def _tree_rounded_reference(case, scale):
+    """The oracle's attention with the kernel's two roundings: the
+    unnormalized probabilities (<= 1) to bf16 for the P.V product (the sum
+    l stays fp32), and the output to bf16."""
+    cu = case["cu_a"].tolist()
+    T, H, d = case["q"].shape
+    out = torch.zeros(T, H, d)
+    for s in range(len(cu) - 1):
+        a, b = cu[s], cu[s + 1]
+        c, r = b - a, int(case["seg_read"][s])
+        k, v = case["k3"][a:b].float(), case["v3"][a:b].float()
+        vis = ref.causal_visible(c, c)
+        if r >= 0:
+            n = int(case["used"][r])
+            k = torch.cat([ref.gather_pages(case["k_rows"], case["table"][r], n).float(), k])
+            v = torch.cat([ref.gather_pages(case["v_rows"], case["table"][r], n).float(), v])
+            vis = torch.cat([torch.ones(c, n, dtype=torch.bool), vis], 1)
+        kk = k.repeat_interleave(H // k.shape[1], 1)
+        vv = v.repeat_interleave(H // v.shape[1], 1)
+        sc = torch.einsum("chd,lhd->hcl", case["q"][a:b].float(), kk) * scale
+        sc = sc.masked_fill(~vis[None], float("-inf"))
+        p = torch.exp(sc - sc.amax(-1, keepdim=True))
+        l = p.sum(-1, keepdim=True)
+        o = torch.einsum("hcl,lhd->chd", p.to(torch.bfloat16).float() / l, vv)
+        out[a:b] = o.to(torch.bfloat16).float()
+    return out
+
+
+def test_tree_attention_sharp_softmax_matches_its_rounding_model():
+    """Q, K, V ~ N(0, 1): peaked probabilities that expose any mismatch of a
+    probability with the wrong key's V. Against the oracle with the kernel's
+    bf16 roundings applied: within one bf16 step of the output (2^-7
+    relative; the kernel rounds probabilities against the running maximum,
+    the model against the final one) plus 2e-3."""
+    case = _tree_case(65, sd=1.0)
+    got = _run_tree(case, fp8=False).float().cpu()
+    want = _tree_rounded_reference(case, 1 / math.sqrt(128))
+    excess = ((got - want).abs() - (2.0 ** -7 * want.abs() + 2e-3)).max().item()
+    assert excess <= 0, f"beyond one bf16 step by {excess}"
+
+
+def test_tree_attention_is_deterministic():
+    case = _tree_case(66, sd=1.0)
+    first = _run_tree(case, fp8=False).cpu()
+    for _ in range(3):
+        assert torch.equal(_run_tree(case, fp8=False).cpu(), first)
+
+
+@pytest.mark.parametrize("ue8m0", [False, True])
+def test_tree_attention_fp8_matches_quantized_bf16(ue8m0):
+    case = _tree_case(63)
+    out = _run_tree(case, fp8=False)
+    q_ref, s_ref = K.group_quant(out.view(case["T"], -1), ue8m0)
+    q, s = _run_tree(case, fp8=True, ue8m0=ue8m0)
+    assert torch.equal(s.cpu(), s_ref.cpu())
+    assert torch.equal(q.view(torch.uint8).cpu(), q_ref.view(torch.uint8).cpu())
+
+
+def test_tree_attention_agrees_with_the_two_pass_form():
+    """Call A + call B + merge_attn_quant (the reference's three launches,
+    with their bf16 roundings) against the fused kernel. The merge's bf16
+    weights and bf16 partial outputs move values by ~0.4% relative, which
+    after two 1x128 quantizations (on slightly different grids) leaves the
+    CPU oracle's own two forms 1.6% apart in relative L2 with 2.2% of values
+    beyond one e4m3 step; the bars are 3% and 5%."""
+    case = _tree_case(64, nan_unread=False)
+    T = case["T"]
+    kp = layout.k_pool_from_rows(case["k_rows"]).to(DEV)
+    vp = layout.v_pool_from_rows(case["v_rows"]).to(DEV)
+    q3, k3, v3 = case["q"].to(DEV), case["k3"].to(DEV), case["v3"].to(DEV)
+    cu_a = case["cu_a"].to(DEV)
+    scale = 1 / math.sqrt(128)
+    a_len = cu_a[1:] - cu_a[:-1]
+    out_a, lse_a = K.attention(q3, cu_a, a_len.to(torch.int32), n_queries=T,
+                               max_q=int(a_len.max()), softmax_scale=scale, causal=True,
+                               k_rows=k3, v_rows=v3, cu_k=cu_a, n_kv=8, want_lse=True)
+    # call B: the readers of each node stacked into one sequence per node
+    sr = case["seg_read"]
+    rows, cu_q, used, tab = [], [0], [], []
+    for r in range(case["table"].shape[0]):
+        mine = [torch.arange(int(case["cu_a"][s]), int(case["cu_a"][s + 1]))
+                for s in range(len(sr)) if int(sr[s]) == r]
+        if not mine:
+            continue
+        rows.append(torch.cat(mine))
+        cu_q.append(cu_q[-1] + rows[-1].numel())
+        used.append(int(case["used"][r]))
+        tab.append(case["table"][r])
+    rows = torch.cat(rows)
+    source = torch.full((T,), -1, dtype=torch.int32)
+    source[rows] = torch.arange(rows.numel(), dtype=torch.int32)
+    out_b, lse_b = K.attention(q3, torch.tensor(cu_q, dtype=torch.int32, device=DEV),
+                               torch.tensor(used, dtype=torch.int32, device=DEV),
+                               n_queries=rows.numel(), max_q=max(cu_q[i + 1] - cu_q[i] for i in range(len(used))),
+                               softmax_scale=scale, causal=False, k_pool=kp, v_pool=vp,
+                               table=torch.stack(tab).to(DEV), q_rows=rows.to(DEV), n_kv=8,
+                               want_lse=True)
+    q2, s2 = K.merge_attn_quant(out_a, lse_a, out_b, lse_b, source.to(DEV))
+    q1, s1 = _run_tree(case, fp8=True)
+    two = ref.dequant_rows(q2.cpu(), s2.cpu())
+    one = ref.dequant_rows(q1.cpu(), s1.cpu())
+    # the bf16 intermediates of the two-pass form move a value by ~2^-8
+    # relative, which can flip its e4m3 rounding by one step (2^-3 relative)
+    rel = ((two - one).norm() / one.norm()).item()
+    assert rel < 0.03, f"relative L2 {rel}"
+    # one e4m3 step at each value, in units of its group's scale: 2^(e-3)
+    # for normal values (e = floor(log2 |x|)), 2^-9 below 2^-6
+    scale = torch.maximum(s1.cpu(), s2.cpu()).repeat_interleave(128, dim=1)
+    mag = torch.maximum(two.abs(), one.abs()) / scale
+    step = torch.where(mag >= 2.0 ** -6, torch.exp2(torch.floor(torch.log2(mag.clamp(min=1e-30))) - 3),
+                       torch.full_like(mag, 2.0 ** -9)) * scale
+    beyond = ((two - one).abs() > step * 1.001).float().mean().item()
+    assert beyond < 0.05, f"values off by more than one e4m3 step: {beyond}"

@@ -206,6 +206,54 @@ def test_merge_of_a_split_key_set_equals_attention_over_all_keys():
     assert torch.equal(passed, out_a.to(torch.bfloat16).float())
 
 
+def test_tree_attention_equals_sdpa_per_segment_and_the_exact_lse_merge():
+    # segments with and without a read, a partial last node page, permuted
+    # physical pages; pinned against torch's scaled_dot_product_attention
+    # over [node keys | own keys] with the node fully visible and the own
+    # part causal, and against the LSE combination of call A and call B in
+    # fp32 (sigmoid weights, no bf16 rounding)
+    g = gen(13)
+    H, KH, d, page = 8, 2, 128, 16
+    n_pages = 12
+    k_pool = torch.randn(n_pages * page, KH, d, generator=g).to(torch.bfloat16)
+    v_pool = torch.randn(n_pages * page, KH, d, generator=g).to(torch.bfloat16)
+    perm = torch.randperm(n_pages, generator=g).to(torch.int32)
+    table = torch.stack([perm[:4], perm[4:8]])
+    used = torch.tensor([37, 64], dtype=torch.int32)
+    cu_a = [0, 5, 9, 30, 31]
+    seg_read = torch.tensor([0, -1, 1, 0], dtype=torch.int32)
+    T = cu_a[-1]
+    q = (torch.randn(T, H, d, generator=g) * 0.3).to(torch.bfloat16)
+    k3 = torch.randn(T, KH, d, generator=g).to(torch.bfloat16)
+    v3 = torch.randn(T, KH, d, generator=g).to(torch.bfloat16)
+    scale = 1 / math.sqrt(d)
+    got = ops.tree_attention(q, k3, v3, cu_a, seg_read, k_pool, v_pool, table, used, scale)
+    out_a, lse_a = ops.varlen_attention(q, k3, v3, cu_a, scale, causal=True)
+    for s in range(len(cu_a) - 1):
+        a, b = cu_a[s], cu_a[s + 1]
+        r = int(seg_read[s])
+        qs = q[a:b].float().transpose(0, 1)                       # [H, c, d]
+        own_k = k3[a:b].float().repeat_interleave(H // KH, 1).transpose(0, 1)
+        own_v = v3[a:b].float().repeat_interleave(H // KH, 1).transpose(0, 1)
+        mask = torch.ones(b - a, b - a, dtype=torch.bool).tril()
+        if r >= 0:
+            n = int(used[r])
+            rows = table[r][torch.arange(n) // page].long() * page + torch.arange(n) % page
+            nk = k_pool[rows].float().repeat_interleave(H // KH, 1).transpose(0, 1)
+            nv = v_pool[rows].float().repeat_interleave(H // KH, 1).transpose(0, 1)
+            own_k, own_v = torch.cat([nk, own_k], 1), torch.cat([nv, own_v], 1)
+            mask = torch.cat([torch.ones(b - a, n, dtype=torch.bool), mask], 1)
+            # call B alone, merged with call A by the exact LSE rule
+            out_b, lse_b = ops.attend(q[a:b], k_pool[rows], v_pool[rows], scale,
+                                      torch.ones(b - a, n, dtype=torch.bool))
+            w = torch.sigmoid(lse_b - lse_a[:, a:b]).T[..., None]
+            merged = out_a[a:b] + (out_b - out_a[a:b]) * w
+            assert (got[a:b] - merged).abs().max() < 1e-5
+        want = torch.nn.functional.scaled_dot_product_attention(
+            qs, own_k, own_v, attn_mask=mask, scale=scale).transpose(0, 1)
+        assert (got[a:b] - want).abs().max() < 1e-5, f"segment {s}"
+
+
 # ---------------------------------------------------------------- readout
 
 def test_answer_bits_reference_literal_case_and_strict_ties():
