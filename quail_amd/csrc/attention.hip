@@ -481,7 +481,7 @@ __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int a = 0; a < 16; ++a) acc_o[db][a] = 0.f;
-  float m_run = -INFINITY;
+  float m_run = -1e30f;   // finite floor: see the softmax note in the tile loop
   float l_run = 0.f;
   float pg_next = __builtin_bit_cast(float, pg2);  // page id for the DMA of tile t+2
 
@@ -492,7 +492,11 @@ __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
     asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     asm volatile("" : "+v"(pg_next));
     const int page_t2 = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, pg_next));
-    __syncthreads();  // stage t visible to all; stage t-1 free
+    // stage t visible to all (every wave waited for its share above); stage
+    // t-1 free. A plain barrier: __syncthreads' fence would also wait for
+    // the DMA of tile t+1.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
     load_page_id(t + 3, pg_next);
     dma_tile(t + 2, page_t2);
 
@@ -512,7 +516,8 @@ __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
           if (8 * lh + e >= valid) v.set(e, 0);
         store8(vp, v);
       }
-      __syncthreads();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
     }
 
     // ---- S^T = K Q^T ---------------------------------------------------------
@@ -527,31 +532,45 @@ __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
           *reinterpret_cast<const bf16x8_t*>(krow + (((2 * st + half) ^ ksw) * 16));
       sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[st], sacc, 0, 0, 0);
     }
-    // ---- mask, scale, online softmax (log2 domain) -------------------------
-    float tmax = -INFINITY;
+    // ---- mask (boundary tiles only), online softmax (log2 domain) ---------
+    // every key of a tile is visible to every row when the tile ends before
+    // both the sequence and the first row's causal limit
+    const int first_lim = CAUSAL ? kv_len - count + i0 + 1 : kv_len;
+    if (key0 + BKV > min(kv_len, first_lim)) {
 #pragma unroll
-    for (int a = 0; a < 16; ++a) {
-      const int key = key0 + kperm(8 * (a >> 2) + 4 * half + (a & 3));
-      const float v = key < lim ? sacc[a] * p.scale_log2 : -INFINITY;
-      sacc[a] = v;
-      tmax = fmaxf(tmax, v);
+      for (int a = 0; a < 16; ++a) {
+        const int key = key0 + kperm(8 * (a >> 2) + 4 * half + (a & 3));
+        if (key >= lim) sacc[a] = -INFINITY;
+      }
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+    float tmax = sacc[0];
+#pragma unroll
+    for (int a = 1; a < 16; ++a) tmax = fmaxf(tmax, sacc[a]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;
+    // The running maximum moves only when a row's tile maximum exceeds it by
+    // more than 8 (probabilities up to 2^8 against it are exact in the fp32
+    // sums and lose nothing in bf16), so the rescale of the accumulator is
+    // skipped on most tiles; m_run starts at a finite floor, so exp2 of a
+    // masked score is 0 and no -inf arithmetic needs a guard.
+    const bool grow = tmax > m_run + 8.0f;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float m_new = grow ? tmax : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int a = 0; a < 16; ++a) acc_o[db][a] *= alpha;
+    }
     float psum = 0.f;
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
-      const float e = (m_new == -INFINITY) ? 0.f : exp2f(sacc[a] - m_new);
+      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[a], p.scale_log2, -m_run));
       sacc[a] = e;
       psum += e;
     }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int a = 0; a < 16; ++a) acc_o[db][a] *= alpha;
+    l_run += psum;
 
     // ---- O^T += V^T P^T over the tile's two pages ----------------------------
 #pragma unroll
@@ -719,23 +738,27 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
   // keys 16 pit .. 16 pit + 15 of a tile, as four 1 KiB pieces -------------
   const int region = wave >> 1;
   const int pit = wave & 1;
-  uint32_t voff_node[4], voff_own[4];
   const uint32_t row_bytes = (uint32_t)p.ld_kv * 2u;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int P = 1024 * c + 16 * lane;  // byte position in the wave's 4 KiB block
-    const int r16 = P >> 8, pc = (P >> 4) & 15;
-    if (region == 0) {
-      voff_node[c] = (uint32_t)(r16 * 256 + ((pc ^ kswz(16 * pit + r16)) * 16));
-      voff_own[c] = (uint32_t)r16 * row_bytes + (uint32_t)hk * 256u +
-                    (uint32_t)((pc ^ kswz(16 * pit + r16)) * 16);
-    } else {
-      const int d = P >> 5, ph = (P >> 4) & 1;
-      voff_node[c] = (uint32_t)(d * 32 + ((ph ^ ((d >> 3) & 1)) * 16));
-      voff_own[c] = (uint32_t)r16 * row_bytes + (uint32_t)hk * 256u +
-                    (uint32_t)((pc ^ vswz(16 * pit + r16)) * 16);
-    }
-  }
+  // Lane byte offsets of DMA piece c (bytes 1024 c + 16 lane of the wave's
+  // 4 KiB block): key r16 = 4c + lane/16 of the wave's 16, physical chunk
+  // lane % 16, which holds logical chunk (lane % 16) ^ swizzle(key). K's
+  // swizzle kswz(16 pit + r16) = r16 ^ pit; own V's vswz = 4 (r16 % 4) =
+  // 4 (lane / 16); a node V^T row d = 32c + lane/2 swaps its halves when
+  // (d / 8) is odd, i.e. when (lane / 16) is odd. Computed per piece from
+  // the lane, to keep registers for the tile loop.
+  const int l16 = lane >> 4, pc = lane & 15;
+  const uint32_t k_chunk = (uint32_t)((pc ^ l16 ^ pit) * 16);  // XOR 64 c per piece
+  const uint32_t own_v_chunk = (uint32_t)((pc ^ (4 * l16)) * 16);
+  const uint32_t node_v_off = (uint32_t)((lane >> 1) * 32 + (((lane & 1) ^ (l16 & 1)) * 16));
+  const uint32_t own_row = (uint32_t)l16 * row_bytes + (uint32_t)hk * 256u;
+  auto voff_node = [&](int c) __attribute__((always_inline)) {
+    return region == 0 ? (uint32_t)((4 * c + l16) * 256) + (k_chunk ^ (uint32_t)(64 * c))
+                       : node_v_off + (uint32_t)(1024 * c);
+  };
+  auto voff_own = [&](int c) __attribute__((always_inline)) {
+    return own_row + (uint32_t)(4 * c) * row_bytes +
+           (region == 0 ? (k_chunk ^ (uint32_t)(64 * c)) : own_v_chunk);
+  };
   const uint16_t* pool = region ? p.v_pool : p.k_pool;
   const uint16_t* own_rows = region ? p.v_rows : p.k_rows;
   const pi32x4 rtab = attn_rsrc(p.table, r >= 0 ? (uint32_t)p.n_reads * (uint32_t)p.table_width * 4u : 0u);
@@ -767,7 +790,7 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
             "s_mov_b32 m0, %0\n\t"
             "buffer_load_dwordx4 %1, %2, 0 offen lds"
             :
-            : "s"(base + 1024 * c), "v"(voff_node[c]), "s"(rs)
+            : "s"(base + 1024 * c), "v"(voff_node(c)), "s"(rs)
             : "memory", "m0");
     } else {
       // own keys 32 (t - n1) + 16 pit + 0..15: chunk rows q0 + those keys;
@@ -783,7 +806,7 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
             "s_mov_b32 m0, %0\n\t"
             "buffer_load_dwordx4 %1, %2, 0 offen lds"
             :
-            : "s"(base + 1024 * c), "v"(voff_own[c]), "s"(rs)
+            : "s"(base + 1024 * c), "v"(voff_own(c)), "s"(rs)
             : "memory", "m0");
     }
   };
@@ -822,17 +845,23 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int a = 0; a < 16; ++a) acc_o[db][a] = 0.f;
-  float m_run = -INFINITY;
+  float m_run = -1e30f;   // finite floor: see the softmax note in the tile loop
   float l_run = 0.f;
   float pg_next = __builtin_bit_cast(float, pg2);
 
   // own-tile P.V operand addresses (see the note above the kernel): lane
   // group G = lane / 16 covers d = 32 db + 16 (G % 2) + lane % 16 and keys
   // 16 pt + 8 (G / 2) + 4 u + 0..3; lane addresses key + (lane % 16) / 4
+  // byte offset of that address within the tile's V rows at db = 0: key
+  // tr_key's row, logical chunk 2 (G % 2) + (lane % 4) / 2 XOR the row's
+  // vswz (a lane constant: vswz(key) = 4 (key % 4) and 16 pt + 4 u keeps
+  // key % 4), half (lane % 2); block db only XORs 4 db into the chunk, i.e.
+  // 64 db into the byte offset
   const int gi = lane & 15;
   const int tr_key = 8 * (lane >> 5) + (gi >> 2);
-  const int tr_chunk = 2 * ((lane >> 4) & 1) + ((gi & 3) >> 1);
-  const int tr_byte = (gi & 1) * 8;
+  const uint32_t tr_off = (uint32_t)(tr_key * 256 +
+                                     (((2 * ((lane >> 4) & 1) + ((gi & 3) >> 1)) ^ vswz(tr_key)) * 16) +
+                                     (gi & 1) * 8);
 
   const int kq = kperm(col);
   // one 32-key tile; NODE is the phase (the two phases' P.V operands differ)
@@ -841,7 +870,11 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
     asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     asm volatile("" : "+v"(pg_next));
     const int page_t2 = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, pg_next));
-    __syncthreads();  // stage t visible to all; stage t-1 free
+    // stage t visible to all (every wave waited for its share above); stage
+    // t-1 free. A plain barrier: __syncthreads' fence would also wait for
+    // the DMA of tile t+1.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
     load_page_id(t + 3, pg_next);
     dma_tile(t + 2, page_t2);
 
@@ -861,7 +894,8 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
           if (8 * lh + e >= valid) v.set(e, 0);
         store8(vp, v);
       }
-      __syncthreads();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
     }
 
     // ---- S^T = K Q^T ---------------------------------------------------------
@@ -876,32 +910,46 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
           *reinterpret_cast<const bf16x8_t*>(krow + (((2 * st + half) ^ ksw) * 16));
       sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, qf[st], sacc, 0, 0, 0);
     }
-    // ---- mask, scale, online softmax (log2 domain) -------------------------
-    const int lim = node ? node_keys : my_i + 1;
-    float tmax = -INFINITY;
+    // ---- mask (boundary tiles only), online softmax (log2 domain) ---------
+    // a node tile needs the mask only past node_keys; an own tile only where
+    // it reaches past the q-tile's first row (the causal diagonal)
+    const bool need_mask = node ? key0 + BKV > node_keys : key0 + BKV - 1 > i0;
+    if (need_mask) {
+      const int lim = node ? node_keys : my_i + 1;
 #pragma unroll
-    for (int a = 0; a < 16; ++a) {
-      const int key = key0 + kperm(8 * (a >> 2) + 4 * half + (a & 3));
-      const float v = key < lim ? sacc[a] * p.scale_log2 : -INFINITY;
-      sacc[a] = v;
-      tmax = fmaxf(tmax, v);
+      for (int a = 0; a < 16; ++a) {
+        const int key = key0 + kperm(8 * (a >> 2) + 4 * half + (a & 3));
+        if (key >= lim) sacc[a] = -INFINITY;
+      }
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+    float tmax = sacc[0];
+#pragma unroll
+    for (int a = 1; a < 16; ++a) tmax = fmaxf(tmax, sacc[a]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * p.scale_log2;
+    // The running maximum moves only when a row's tile maximum exceeds it by
+    // more than 8 (probabilities up to 2^8 against it are exact in the fp32
+    // sums and lose nothing in bf16), so the rescale of the accumulator is
+    // skipped on most tiles; m_run starts at a finite floor, so exp2 of a
+    // masked score is 0 and no -inf arithmetic needs a guard.
+    const bool grow = tmax > m_run + 8.0f;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float m_new = grow ? tmax : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int a = 0; a < 16; ++a) acc_o[db][a] *= alpha;
+    }
     float psum = 0.f;
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
-      const float e = (m_new == -INFINITY) ? 0.f : exp2f(sacc[a] - m_new);
+      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[a], p.scale_log2, -m_run));
       sacc[a] = e;
       psum += e;
     }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int a = 0; a < 16; ++a) acc_o[db][a] *= alpha;
+    l_run += psum;
 
     // ---- O^T += V^T P^T over the tile's two 16-key steps ---------------------
 #pragma unroll
@@ -923,12 +971,10 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
           ts16x4 part[2];
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
-            const int key = 16 * pt + 4 * u + tr_key;
-            const int chunk = (4 * db + tr_chunk) ^ vswz(key);
             auto a = (__attribute__((address_space(3))) ts16x4*)(
                 (__attribute__((address_space(3))) uint8_t*)(
                     (const __attribute__((address_space(3))) void*)(st_base + HALF)) +
-                key * 256 + chunk * 16 + tr_byte);
+                (16 * pt + 4 * u) * 256 + (tr_off ^ (uint32_t)(64 * db)));
             part[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(a);
           }
           const ts16x4 x0 = part[0], x1 = part[1];
