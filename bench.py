@@ -216,14 +216,15 @@ def main():
     ap.add_argument("--steps", type=int, default=2)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--workload", default="aiif-4b",
-                    choices=["aiif-4b", "aiif-32b", "join-4b", "attn-c1"],
+                    choices=["aiif-4b", "aiif-32b", "join-4b", "attn-c1", "gemm-c2"],
                     help="aiif-4b: Qwen3-4B, 64-token instruction, lognormal docs (median "
                          "180, cap 1024); aiif-32b: Qwen3-32B, 128-token instruction, docs "
                          "uniform in [1024, 4096]; join-4b: Qwen3-4B AI join, anchors = "
                          "48-token root + left doc (lognormal median 120), partners = right "
                          "docs (lognormal median 120, cap 512), tree attention; attn-c1: "
                          "one attention layer, 64 rows sharing a 256-token prefix of a "
-                         "paged arena, suffixes U[32, 256], 32/8 heads")
+                         "paged arena, suffixes U[32, 256], 32/8 heads; gemm-c2: the fp8 "
+                         "block-scaled GEMM at the four Qwen3-4B shapes, M = 16384")
     ap.add_argument("--anchors", type=int, default=32,
                     help="join-4b: left rows (anchors); 256 is the full 256 x 256 join")
     ap.add_argument("--partners", type=int, default=256, help="join-4b: right rows")
@@ -255,6 +256,9 @@ def main():
         return
     if args.workload == "attn-c1":
         attention_bench(args)
+        return
+    if args.workload == "gemm-c2":
+        gemm_bench(args)
         return
     if args.attention is None:
         args.attention = "unified"
@@ -377,6 +381,101 @@ def main():
                       "calls": k["attn_kinds"]},
         "answers_true": int(sum(answers)), "deterministic_across_steps": steady,
         "build_s": round(build_s, 1),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+GEMM_SHAPES = (("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 19456, 2560),
+               ("down", 2560, 9728))
+
+
+def gemm_bench(args):
+    """The fp8 block-scaled GEMM at the Qwen3-4B projection shapes, M = 16384.
+
+    W ~ N(0, 0.02) quantized to e4m3 with fp32 128x128 block scales
+    (amax/448); X ~ N(0, 1) quantized with 1x128 per-token scales; bf16
+    out (the gate_up shape also runs the fused SiLU-gate + fp8 quant
+    epilogue the model uses). Each launch is timed with HIP events on the
+    launch stream.
+    """
+    import torch
+
+    from oracle import ops as oops
+    from quail_amd import kernels as K
+
+    M = 16384
+    g = torch.Generator().manual_seed(args.seed)
+    stream = torch.cuda.current_stream()
+    iters = max(args.steps, 1) * 10
+    shapes, total_f, total_ms, cpu = {}, 0.0, 0.0, None
+    x = torch.randn(M, 9728, generator=g)
+    for name, N, Kd in GEMM_SHAPES:
+        w = torch.randn(N, Kd, generator=g) * 0.02
+        wq, ws = oops.quantize_weight_blocks(w)
+        xq, xs = oops.group_quant(x[:, :Kd])
+        a = xq.to("cuda")
+        sa = K.col_major_scales(M, Kd, "cuda")
+        sa.copy_(xs.to("cuda"))
+        wq, ws = wq.to("cuda"), ws.to("cuda")
+        variants = [("bf16 out", lambda: K.fp8_gemm_nt(a, sa, wq, ws))]
+        if name == "gate_up":
+            variants.append(("silu+fp8 out", lambda: K.fp8_gemm_silu_quant(a, sa, wq, ws)))
+        flops = 2.0 * M * N * Kd
+        rec = {}
+        for label, fn in variants:
+            for _ in range(max(args.warmup, 1) * 3):
+                fn()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(iters):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / iters
+            rec[label] = dict(ms=round(ms, 4), tflops=round(flops / ms / 1e9, 1),
+                              frac=round(flops / ms / 1e9 / FP8_PEAK_TFLOPS, 4))
+        total_f += flops
+        total_ms += rec["bf16 out"]["ms"]
+        # parity on a row sample: the oracle's exact block sums
+        rows = torch.arange(0, M, M // 64)
+        got = K.fp8_gemm_nt(a, sa, wq, ws)[rows.to("cuda")].float().cpu()
+        want = oops.fp8_gemm(xq[rows], xs[rows].contiguous(), wq.cpu(), ws.cpu()).float()
+        rec["rel_l2_vs_oracle_64_rows"] = round(((got - want).norm() / want.norm()).item(), 6)
+        shapes[name] = dict(N=N, K=Kd, gflop=round(flops / 1e9, 1), **rec)
+    if not args.no_cpu_baseline:
+        threads = min(16, len(os.sched_getaffinity(0)))
+        torch.set_num_threads(threads)
+        name, N, Kd = GEMM_SHAPES[0]
+        rows = 1024
+        w = torch.randn(N, Kd, generator=g) * 0.02
+        wq, ws = oops.quantize_weight_blocks(w)
+        xq, xs = oops.group_quant(x[:rows, :Kd])
+        t0 = time.perf_counter()
+        ref = oops.dequant_rows(xq, xs) @ oops.dequant_weight(wq, ws).T
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": round(2.0 * rows * N * Kd / cpu_s / 1e12, 4), "unit": "TFLOP/s",
+               "cores": threads, "kind": "port",
+               "sample": f"oracle fp8 GEMM (dequantize with block scales, fp32 matmul), "
+                         f"qkv shape with M = {rows}: {cpu_s:.2f} s"}
+        del ref
+    achieved = total_f / total_ms / 1e9
+    line = {
+        "metric": "fp8 block-scaled GEMM TFLOP/s at the Qwen3-4B shapes (M = 16384) on 1 GPU; "
+                  "% of fp8 MFMA peak",
+        "value": round(achieved, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": iters,
+        "warmup": max(args.warmup, 1) * 3, "ms_per_step": round(total_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8",
+        "data": "synthetic",
+        "config": {"workload": "fp8 block-scaled GEMM sweep, M = 16384, (N, K) in "
+                               "{(6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728)}, "
+                               "fp32 128x128 weight / 1x128 activation scales, bf16 out"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": FP8_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
+                     "traffic": None, "kernel": "qh fp8_gemm_kernel"},
+        "shapes": shapes,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
