@@ -18,20 +18,29 @@
 //     row segment lives in one wave (what the fused SiLU epilogue needs).
 //   - the workgroup walks its tiles as one stream of 128-deep K steps. Weight
 //     blocks reach LDS by DMA (buffer_load ... lds) NS-1 = 3 steps ahead into a
-//     4-stage ring; each wave loads its own activation fragments and the
-//     scales straight into VGPRs PA = 2 steps ahead. Loads cross tile
-//     boundaries, so a tile's first blocks arrive during the previous tile.
+//     4-stage ring. Each wave DMAs its own 32 tokens' activation block one step
+//     ahead into a 4 KiB LDS region only it touches, and loads the scales
+//     straight into VGPRs two steps ahead. Loads cross tile boundaries, so a
+//     tile's first blocks arrive during the previous tile. Every load is a DMA
+//     of whole 128-byte rows: loading activation fragments straight into
+//     VGPRs touches 16 half-used lines per instruction and measured ~25 % of
+//     the step.
 //   - every wave issues exactly LOADS = 12 vector-memory loads per step, all
-//     as inline asm, one between consecutive MFMA pairs; the wait at the top
-//     of step s is vmcnt(12): the loads issued since step s's activations
-//     are exactly the previous step's twelve. A wait counts stores too, and
-//     stores may complete out of order with loads, so the count is never
-//     raised for them: a tile's epilogue takes the next step's wait before
-//     it issues its stores, the next step skips its wait, and the stores
-//     have that whole step to drain before the following wait.
+//     as inline asm, one between consecutive MFMA pairs, in the order
+//     activation DMA (step s+1), weight DMA (s+3), scales (s+2). The wait at
+//     the end of step s is vmcnt(8): everything but this step's weight DMA
+//     and scales has landed, the activation block of step s+1 included, whose
+//     fragments are then read into VGPRs. A wait counts stores too; loads
+//     complete in order among themselves, so a count that leaves only the
+//     last eight loads in flight also leaves no older load in flight,
+//     whatever the stores do. A tile's epilogue issues its stores right after
+//     that wait, so they have a whole step to drain before the next one.
 //   - one barrier per step: it publishes stage s (every wave's DMA share has
 //     landed) and frees stage s-1 for the DMA of step s+3. The first two
 //     weight fragments of step s+1 are read at the end of step s.
+//   - the epilogue stages its output through the wave's activation region,
+//     after that region's fragments for the next step are in VGPRs and before
+//     the next step's activation DMA overwrites it.
 //   - tiles are ordered so each XCD's L2 works on a contiguous group of them.
 #include "common.h"
 
@@ -49,9 +58,9 @@ constexpr int BM = 256;         // tile tokens
 constexpr int BR = 256;         // tile weight rows
 constexpr int BK = 128;         // K block: one MFMA, one scale block
 constexpr int NS = 4;           // weight stages in LDS
-constexpr int PA = 2;           // activation blocks in flight ahead
+constexpr int PA = 2;           // scale blocks in flight ahead
 constexpr int STAGE = BR * BK;  // 32 KiB
-constexpr int EPI_BYTES = 2304; // per-wave LDS slice for staging epilogue stores
+constexpr int A_WAVE = 32 * BK; // 4 KiB: a wave's 32 tokens of one K block
 constexpr int LOADS = 12;       // vector-memory loads per wave per step
 constexpr int XCDS = 8;
 enum { kStoreBf16 = 0, kSiluQuant = 1 };
@@ -92,8 +101,8 @@ __device__ __forceinline__ float silu_mul_bf16(float gate_acc, float up_acc) {
 template <int EPI>
 __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
   using namespace gemm;
-  // weight stages, then one epilogue slice per wave
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE + 8 * EPI_BYTES];
+  // weight stages, then one activation region per wave (160 KiB in all)
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * STAGE + 8 * A_WAVE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -168,69 +177,66 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
         : "memory", "m0");
   };
 
-  // Activation fragments: lane reads token 32*wave + 16*j + lane%16 of the
-  // tile, K bytes [16g, 16g+16) and [64+16g, 64+16g+16) of the block (the
-  // weight fragments use the same K order). Tokens past M lie outside the
-  // descriptor and read zero. Then the two activation scales of the lane's
-  // tokens and the two weight-block scales of the tile.
-  const uint32_t offa = (uint32_t)(32 * wave + (lane & 15)) * (uint32_t)lda + 16u * g;
+  // Activation DMA: instruction i (0..3) fills rows 8i .. 8i+7 of the wave's
+  // region, i.e. tokens 32*wave + 8i + lane/8 of the tile, with the weight
+  // blocks' chunk swizzle. Tokens past M lie outside the descriptor and read
+  // zero. Then the two activation scales of the lane's tokens and the two
+  // weight-block scales of the tile, straight into VGPRs.
+  uint8_t* const areg = lds + NS * STAGE + wave * A_WAVE;
+  const uint32_t offa = (uint32_t)(32 * wave + (lane >> 3)) * (uint32_t)lda +
+                        (uint32_t)((((lane & 7) ^ (lane >> 3)) & 7) * 16);
   const uint32_t srow = 4u * (uint32_t)(32 * wave + (lane & 15));
   const i32x4 rsa = buffer_rsrc(p.sa, (uint32_t)nk * (uint32_t)M * 4u);
   const i32x4 rsb = buffer_rsrc(p.sb, (uint32_t)(p.N / 128) * (uint32_t)nk * 4u);
   struct ALoad {
     i32x4 ra;
-    uint32_t k0, k1, ks, kw0, kw1;
+    uint32_t k0, ks, kw0, kw1;
   };
   auto a_args = [&](const Cursor& c) __attribute__((always_inline)) {
     ALoad L;
     const int m0 = c.tm * BM;
     L.ra = buffer_rsrc(p.A + (long)m0 * lda, (uint32_t)((long)min(M - m0, BM) * lda));
     L.k0 = (uint32_t)c.kb * BK;
-    L.k1 = L.k0 + 16u * (uint32_t)lda;
     L.ks = ((uint32_t)c.kb * (uint32_t)M + (uint32_t)m0) * 4u;
     L.kw0 = ((uint32_t)(weight_row(c.tn, 0) / 128) * (uint32_t)nk + (uint32_t)c.kb) * 4u;
     L.kw1 = ((uint32_t)(weight_row(c.tn, 1) / 128) * (uint32_t)nk + (uint32_t)c.kb) * 4u;
     return L;
   };
-  auto a_load = [&](const ALoad& L, int op, i32x4* lo, i32x4* hi, float* sv, float* wv) __attribute__((always_inline)) {
+  auto adma = [&](const ALoad& L, int i) __attribute__((always_inline)) {
+    const uint32_t dst = lds_addr(areg + i * 1024);
+    const uint32_t so = L.k0 + (uint32_t)(8 * i) * (uint32_t)lda;
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "buffer_load_dwordx4 %1, %2, %3 offen lds"
+        :
+        : "s"(dst), "v"(offa), "s"(L.ra), "s"(so)
+        : "memory", "m0");
+  };
+  auto s_load = [&](const ALoad& L, int op, float* sv, float* wv) __attribute__((always_inline)) {
     switch (op) {
       case 0:
-        asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen"
-                     : "=v"(lo[0]) : "v"(offa), "s"(L.ra), "s"(L.k0) : "memory");
-        break;
-      case 1:
-        asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen offset:64"
-                     : "=v"(hi[0]) : "v"(offa), "s"(L.ra), "s"(L.k0) : "memory");
-        break;
-      case 2:
-        asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen"
-                     : "=v"(lo[1]) : "v"(offa), "s"(L.ra), "s"(L.k1) : "memory");
-        break;
-      case 3:
-        asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen offset:64"
-                     : "=v"(hi[1]) : "v"(offa), "s"(L.ra), "s"(L.k1) : "memory");
-        break;
-      case 4:
         asm volatile("buffer_load_dword %0, %1, %2, %3 offen"
                      : "=v"(sv[0]) : "v"(srow), "s"(rsa), "s"(L.ks) : "memory");
         break;
-      case 5:
+      case 1:
         asm volatile("buffer_load_dword %0, %1, %2, %3 offen offset:64"
                      : "=v"(sv[1]) : "v"(srow), "s"(rsa), "s"(L.ks) : "memory");
         break;
-      case 6:
+      case 2:
         asm volatile("buffer_load_dword %0, off, %1, %2"
                      : "=v"(wv[0]) : "s"(rsb), "s"(L.kw0) : "memory");
         break;
-      case 7:
+      case 3:
         asm volatile("buffer_load_dword %0, off, %1, %2"
                      : "=v"(wv[1]) : "s"(rsb), "s"(L.kw1) : "memory");
         break;
     }
   };
 
-  // Weight fragment (n-tile i of a stage): lane reads row 16*i + lane%16,
-  // logical chunks g and g+4; row % 8 == lane % 8, so the swizzle is per lane.
+  // Fragment i of a stage or of a wave's activation region: lane reads row
+  // 16*i + lane%16, logical chunks g and g+4; row % 8 == lane % 8, so the
+  // swizzle is per lane. A region's fragments 0 and 1 are the wave's two
+  // 16-token halves.
   const int frow = (lane & 15) * BK;
   const int c_lo = ((g ^ (lane & 7)) & 7) * 16;
   const int c_hi = (((g + 4) ^ (lane & 7)) & 7) * 16;
@@ -248,7 +254,6 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
   for (int i = 0; i < 16; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = zero;
-  i32x4 alo[PA + 1][2], ahi[PA + 1][2];
   float sav[PA + 1][2], sbv[PA + 1][2];
 
   // ---- epilogues --------------------------------------------------------------
@@ -257,8 +262,9 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
   // instruction, which measured ~16k cycles per tile. Instead each wave
   // stages a few rows of its output at a time in its own LDS slice (rows
   // padded so that the writes are bank-conflict free) and stores whole rows,
-  // 16 bytes per lane.
-  uint8_t* slice = lds + NS * STAGE + wave * EPI_BYTES;
+  // 16 bytes per lane. The slice is the wave's activation region, free
+  // between the read of its fragments and the next activation DMA.
+  uint8_t* const slice = areg;
   auto store_bf16 = [&](const Cursor& c) __attribute__((always_inline)) {
     constexpr int ROWB = 512 + 32;  // one 256-column bf16 row + pad
     uint8_t* C = (uint8_t*)p.C;
@@ -341,49 +347,67 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
     else store_bf16(c);
   };
 
-  // ---- prologue: weight stages 0 .. NS-2, activation blocks 0 .. PA-1 ---------
-  Cursor cd, ca, cc;  // DMA (step s+NS-1), activations (s+PA), compute (s)
+  // ---- prologue -----------------------------------------------------------------
+  // weight stages 0 and 1, the activation block and scales of step 0, then
+  // weight stage 2 and the scales of step 1; the wait leaves those last
+  // eight loads in flight
+  Cursor cd, cn, ca, cc;  // weight DMA (step s+3), activation DMA (s+1), scales (s+2), compute (s)
   start(cd);
+  start(cn);
   start(ca);
   start(cc);
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s) {
+  for (int s = 0; s < 2; ++s) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma(cd, s, i);
     advance(cd);
   }
+  {
+    const ALoad L = a_args(cn);
 #pragma unroll
-  for (int s = 0; s < PA; ++s) {
+    for (int i = 0; i < 4; ++i) adma(L, i);
+    advance(cn);
+  }
+  {
     const ALoad L = a_args(ca);
 #pragma unroll
-    for (int op = 0; op < 8; ++op) a_load(L, op, alo[s], ahi[s], sav[s], sbv[s]);
+    for (int op = 0; op < 4; ++op) s_load(L, op, sav[0], sbv[0]);
     advance(ca);
   }
-  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // all but block 1's eight
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dma(cd, 2, i);
+  advance(cd);
+  {
+    const ALoad L = a_args(ca);
+#pragma unroll
+    for (int op = 0; op < 4; ++op) s_load(L, op, sav[1], sbv[1]);
+    advance(ca);
+  }
+  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
   __builtin_amdgcn_s_barrier();
 
-  // carried across steps: the next two weight fragments, and the last product
-  // of the previous step with its scale
+  // carried across steps: the activation fragments and the first two weight
+  // fragments of the step, and the last two products of the previous step
+  // with their scales
+  v8i xa0 = frag(areg, 0), xa1 = frag(areg, 1);
   v8i bf = frag(lds, 0), bn = frag(lds, 1);
-  f32x4 tp = zero;
-  float s_last = 0.f;
-  bool stored = false;  // the previous step ended with an epilogue
+  f32x4 tp0 = zero, tp1 = zero;  // products two and one MFMAs back
+  float s_last0 = 0.f, s_last1 = 0.f;
 
   auto step = [&](auto slot_c, int s) __attribute__((always_inline)) {
     constexpr int slot = decltype(slot_c)::value;
     constexpr int nslot = (slot + PA) % (PA + 1);
-    // step s's activations and scales (issued at step s-2) have landed, and
-    // with them this wave's DMA share of stage s (issued at s-3); the twelve
-    // loads of step s-1 may be in flight. After a tile's epilogue that wait
-    // already ran, before the stores were issued (see below).
-    if (!stored) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-    stored = false;
-    asm volatile(""
-                 : "+v"(alo[slot][0]), "+v"(alo[slot][1]), "+v"(ahi[slot][0]),
-                   "+v"(ahi[slot][1]), "+v"(sav[slot][0]), "+v"(sav[slot][1]),
-                   "+v"(sbv[slot][0]), "+v"(sbv[slot][1]));
+    // stage s: every wave's DMA share landed before its wait at the end of
+    // step s-1; the barrier publishes it and frees stage s-1
+    asm volatile("" : "+v"(sav[slot][0]), "+v"(sav[slot][1]), "+v"(sbv[slot][0]),
+                 "+v"(sbv[slot][1]));
     __builtin_amdgcn_s_barrier();
-    const ALoad L = a_args(ca);
+    // the activation fragments were read from the region at the end of step
+    // s-1 (and an epilogue may have staged through it since): all of that is
+    // done before this step's activation DMA overwrites the region
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const ALoad Ln = a_args(cn);
+    const ALoad Ls = a_args(ca);
     const int dstage = (s + NS - 1) % NS;
     float sc[2][2];  // [token half][weight half]
 #pragma unroll
@@ -393,61 +417,76 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
     }
     const uint8_t* st = lds + (s % NS) * STAGE;
     const uint8_t* st_next = lds + ((s + 1) % NS) * STAGE;
-    const v8i xa[2] = {
-        (v8i){alo[slot][0][0], alo[slot][0][1], alo[slot][0][2], alo[slot][0][3],
-              ahi[slot][0][0], ahi[slot][0][1], ahi[slot][0][2], ahi[slot][0][3]},
-        (v8i){alo[slot][1][0], alo[slot][1][1], alo[slot][1][2], alo[slot][1][3],
-              ahi[slot][1][0], ahi[slot][1][1], ahi[slot][1][2], ahi[slot][1][3]}};
+    const v8i xa[2] = {xa0, xa1};
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       // fragments two n-tiles ahead; the last two are step s+1's first, from
-      // a stage the wait and barrier above already covered
+      // a stage the previous barrier already covered
       const v8i bnn = i < 14 ? frag(st, i + 2) : frag(st_next, i - 14);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const f32x4 t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
             bf, xa[j], zero, 0, 0, 0, 127, 0, 127);
-        // promote the previous product (one MFMA late, so no FMA waits on
-        // the MFMA it reads)
-        const int q = 2 * i + j - 1;
+        // promote the product two MFMAs back: its MFMA finished while the
+        // one in between ran, so the FMAs co-issue with the MFMA pipe
+        // instead of waiting on it (one MFMA back, they wait)
+        const int q = 2 * i + j - 2;
         if (q >= 0) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[q >> 1][q & 1][r] += tp[r] * sc[q & 1][(q >> 1) >> 3];
+          for (int r = 0; r < 4; ++r) acc[q >> 1][q & 1][r] += tp0[r] * sc[q & 1][(q >> 1) >> 3];
         } else {
+          const float sl = q == -2 ? s_last0 : s_last1;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[15][1][r] += tp[r] * s_last;
+          for (int r = 0; r < 4; ++r) acc[15][q + 2][r] += tp0[r] * sl;
         }
-        tp = t;
+        tp0 = tp1;
+        tp1 = t;
       }
-      // the step's twelve loads, one per n-tile: weight DMA for step s+3,
-      // then activations and scales for step s+2
-      if (i < 4) dma(cd, dstage, i);
-      else if (i < 12) a_load(L, i - 4, alo[nslot], ahi[nslot], sav[nslot], sbv[nslot]);
+      // the step's twelve loads, one per n-tile: activation DMA for step
+      // s+1, weight DMA for step s+3, then scales for step s+2
+      if (i < 4) adma(Ln, i);
+      else if (i < 8) dma(cd, dstage, i - 4);
+      else if (i < 12) s_load(Ls, i - 8, sav[nslot], sbv[nslot]);
       bf = bn;
       bn = bnn;
+      // issue order: MFMA, the two fragment reads, the FMAs of the product
+      // two back, MFMA, FMAs. Left alone, the scheduler puts both MFMAs
+      // last and their products' FMAs first in the next group, where they
+      // wait for the MFMAs instead of running beside them.
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
-    s_last = sc[1][1];
+    s_last0 = sc[0][1];
+    s_last1 = sc[1][1];
+    // everything but this step's weight DMA and scales has landed: the
+    // activation block of step s+1, and weight stage s+2 of this wave
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    xa0 = frag(areg, 0);
+    xa1 = frag(areg, 1);
     if (cc.kb == nk - 1) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[15][1][r] += tp[r] * s_last;
-      tp = zero;
-      s_last = 0.f;
-      // A wait counts stores as well as loads, so the epilogue's stores would
-      // hold up the next step's wait until they complete. Take that wait now,
-      // while no store is outstanding, and skip it at the next step: the
-      // stores then have a whole step to drain before the wait after that.
-      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+      for (int r = 0; r < 4; ++r) {
+        acc[15][0][r] += tp0[r] * s_last0;
+        acc[15][1][r] += tp1[r] * s_last1;
+      }
+      tp0 = tp1 = zero;
+      s_last0 = s_last1 = 0.f;
+      // the region is free once the fragments are in VGPRs
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       epilogue(cc);
-      stored = true;
     }
     advance(cc);
+    advance(cn);
     advance(ca);
     advance(cd);
   };
 
   const int S = my_tiles * nk;
-  static_assert(PA == 2, "the step loop is unrolled for three activation slots");
+  static_assert(PA == 2, "the step loop is unrolled for three scale slots");
   for (int s = 0; s < S; s += 3) {
     step(std::integral_constant<int, 0>{}, s);
     if (s + 1 < S) step(std::integral_constant<int, 1>{}, s + 1);

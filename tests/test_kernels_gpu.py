@@ -174,6 +174,18 @@ def test_fp8_gemm_nt_many_tiles(M, N, Kd):
     assert (err <= tol).all(), f"max err {err.max().item()}"
 
 
+def test_fp8_gemm_nt_is_deterministic():
+    """Launches with the same inputs give the same bits: each output has one
+    fixed order of MFMA products and promotions, whatever the timing of the
+    DMA ring, the tile boundaries or the neighbouring workgroups (several
+    tiles per workgroup, a ragged last tile row)."""
+    a, sa, w, sw = _gemm_inputs(14, 8191, 9728, 1280, DEV)
+    first = K.fp8_gemm_nt(a, sa, w, sw)
+    for _ in range(3):
+        again = K.fp8_gemm_nt(a, sa, w, sw)
+        assert torch.equal(first.view(torch.int16), again.view(torch.int16))
+
+
 @pytest.mark.parametrize("M,I,Kd", [(1, 128, 128), (300, 1024, 2560), (517, 9728, 256),
                                     (2048, 9728, 512)])
 @pytest.mark.parametrize("ue8m0", [False, True])
