@@ -232,6 +232,9 @@ def main():
     ap.add_argument("--rows", type=int, default=None,
                     help="rows (default 4096 for aiif-4b, 256 for aiif-32b)")
     ap.add_argument("--layers", type=int, default=None)
+    ap.add_argument("--documents", default="token-store", choices=["token-store", "memory"],
+                    help="aiif workloads: rows read from a memory-mapped Arrow token store "
+                         "file (the reference's scan input) or from in-memory arrays")
     ap.add_argument("--attention", default=None, choices=["unified", "tree"],
                     help="default: unified for filters, tree for the join")
     ap.add_argument("--arena-pages", type=int, default=None)
@@ -286,6 +289,16 @@ def main():
     else:
         instruction, documents, tail = synthetic_filter_workload(args.rows, seed=args.seed,
                                                                  vocab=spec.vocab)
+    store_dir = None
+    if args.documents == "token-store":
+        import tempfile
+        from quail_amd.tokens import TokenStore
+        store_dir = tempfile.mkdtemp(prefix="quail_amd_rows_")
+        import atexit
+        import shutil
+        atexit.register(shutil.rmtree, store_dir, True)
+        documents = TokenStore.from_documents(os.path.join(store_dir, "documents.arrow"),
+                                              documents)
     clock = KernelClock(torch)
     clock.n_q, clock.d, clock.n_kv = spec.n_q, spec.d_head, spec.n_kv
     runner = FilterRunner(model, spec, device_spec=MI355X, n_pages=args.arena_pages,
@@ -355,7 +368,9 @@ def main():
                        + ("128-token shared instruction, docs uniform in [1024, 4096]"
                           if big else "64-token shared instruction, lognormal docs "
                                       "(median 180, cap 1024)")
-                       + f", 24-token tail, {args.attention} attention"),
+                       + f", 24-token tail, {args.attention} attention, "
+                       + ("rows read from a memory-mapped Arrow token store"
+                          if args.documents == "token-store" else "rows in memory")),
                    "rows": args.rows, "layers": spec.layers,
                    "fresh_tokens": stats["fresh_tokens"],
                    "input_tokens": stats["input_tokens"], "chunks": stats.get("chunks"),

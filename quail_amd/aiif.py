@@ -18,7 +18,7 @@ from quail_amd.model import SYNTHETIC_FALSE_IDS, SYNTHETIC_TRUE_IDS
 from quail_amd.qwen3 import Qwen3Pipeline
 from quail_amd.readout import AnswerRows, AsyncAnswers
 from quail_amd.specs import MI355X
-from quail_amd.tokens import prefix_tree
+from quail_amd.tokens import chain_tokens, prefix_tree
 
 
 def lognormal_lengths(n, median, mean, cap, rng):
@@ -52,10 +52,16 @@ def synthetic_filter_workload(n_rows, *, prefix_tokens=64, median=180, mean=230,
 
 
 class RowPrompts:
-    """Row i = instruction + document i (tokens.DocumentPrefixes), materialised once."""
+    """Row i = instruction + document i (tokens.DocumentPrefixes).
+
+    In-memory documents are materialised once; documents read from a token
+    store stay views of the mapped file, chained after the instruction.
+    """
 
     def __init__(self, instruction, documents):
-        self.rows = [np.concatenate([instruction, d]) for d in documents]
+        instruction = np.asarray(instruction, dtype=np.int64)
+        self.rows = [chain_tokens(instruction, d) if hasattr(d, "token_parts")
+                     else np.concatenate([instruction, d]) for d in documents]
 
     def __len__(self):
         return len(self.rows)

@@ -1,4 +1,14 @@
-"""Token views and the prefix tree that decides KV page borrowing.
+"""Token views, the on-disk token store, and the prefix tree that decides
+KV page borrowing.
+
+Token store files are Arrow IPC files, memory mapped, in the reference's
+layout (quail/execution/tokens.py:193-210, :316-319): one record batch per
+source batch with a `__quail_token_ids` large_list<int> column and a
+`__quail_token_count` int64 column, schema metadata quail.kind=token_store;
+a column store holds one copied source column (quail.kind=column_store). A
+document read from a store is a TokenView over the mapped buffer; slicing
+and prefixing build views and chains, and the packer copies the ids once,
+into its pinned staging buffer.
 
 prefix_tree restates quail/execution/tokens.py:514-591 exactly, because the
 tree fixes which pages every document reads:
@@ -12,6 +22,9 @@ tree fixes which pages every document reads:
     while the ancestor itself borrowed at least that many tokens
     (tokens.py:585-589).
 """
+
+import bisect
+import os
 
 import numpy as np
 
@@ -32,7 +45,7 @@ class PrefixTree:
 def _ids(doc):
     if isinstance(doc, np.ndarray):
         return doc.astype(np.int64, copy=False)
-    return np.asarray(list(doc), dtype=np.int64)
+    return token_array(doc).astype(np.int64, copy=False)
 
 
 def _common(a, b) -> int:
@@ -85,3 +98,415 @@ class DocumentPrefixes:
             return [self[i] for i in range(*index.indices(len(self)))]
         doc = np.asarray(self._documents[self._indices[index]], dtype=np.int64)
         return np.concatenate([self._prefix, doc])
+
+
+# ----------------------------------------------------------------- token views
+
+class TokenView:
+    """One contiguous run of token ids backed by an Arrow array (tokens.py:13-42).
+
+    Integer indexing returns a Python int, a unit-step slice another view
+    over the same buffer, numpy() the ids without a copy.
+    """
+
+    def __init__(self, values):
+        self._values = values
+
+    def __len__(self):
+        return len(self._values)
+
+    def __getitem__(self, index):
+        if isinstance(index, slice):
+            start, stop, step = index.indices(len(self))
+            if step != 1:
+                return self.numpy()[index].tolist()
+            return TokenView(self._values.slice(start, max(stop - start, 0)))
+        return self._values[index].as_py()
+
+    def __iter__(self):
+        return iter(self.numpy().tolist())
+
+    def numpy(self):
+        return self._values.to_numpy(zero_copy_only=True)
+
+    def __array__(self, dtype=None, copy=None):
+        a = self.numpy()
+        return a if dtype is None else a.astype(dtype, copy=False)
+
+    @property
+    def arrow_array(self):
+        return self._values
+
+    @property
+    def token_parts(self):
+        return (self,)
+
+
+class TokenChain:
+    """Token parts read in order without copying them (tokens.py:45-100).
+
+    Nested chains flatten and empty parts drop out; a unit-step slice is a
+    chain of the sliced parts.
+    """
+
+    def __init__(self, *parts):
+        flat = []
+        for part in parts:
+            if isinstance(part, TokenChain):
+                flat.extend(part.token_parts)
+            elif len(part):
+                flat.append(part)
+        self._parts = tuple(flat)
+        self._ends = np.cumsum([len(p) for p in self._parts], dtype=np.int64)
+
+    def __len__(self):
+        return int(self._ends[-1]) if len(self._parts) else 0
+
+    def __iter__(self):
+        for part in self._parts:
+            yield from part
+
+    def __getitem__(self, index):
+        n = len(self)
+        if isinstance(index, slice):
+            start, stop, step = index.indices(n)
+            if step != 1:
+                return token_array(self)[index].tolist()
+            out, begin = [], 0
+            for part, end in zip(self._parts, self._ends.tolist()):
+                if end > start and begin < stop:
+                    out.append(part[max(0, start - begin):min(stop, end) - begin])
+                begin = end
+                if begin >= stop:
+                    break
+            return TokenChain(*out)
+        if index < 0:
+            index += n
+        if not 0 <= index < n:
+            raise IndexError(index)
+        which = int(np.searchsorted(self._ends, index, side="right"))
+        begin = int(self._ends[which - 1]) if which else 0
+        return self._parts[which][index - begin]
+
+    def __array__(self, dtype=None, copy=None):
+        a = token_array(self)
+        return a if dtype is None else a.astype(dtype, copy=False)
+
+    @property
+    def token_parts(self):
+        return self._parts
+
+
+def chain_tokens(*parts):
+    return TokenChain(*parts)
+
+
+def token_parts(seq):
+    """The ids of a token sequence as a list of 1-D numpy arrays, views where
+    the source is a mapped buffer (the packer's part-wise read, loop.py:56-63)."""
+    parts = getattr(seq, "token_parts", None)
+    if parts is None:
+        a = np.asarray(seq)
+        return [a.reshape(-1)] if a.size else []
+    out = []
+    for part in parts:
+        if isinstance(part, TokenView):
+            out.append(part.numpy())
+        elif isinstance(part, np.ndarray):
+            out.append(part.reshape(-1))
+        else:
+            out.extend(token_parts(part))
+    return out
+
+
+def token_array(seq):
+    """A sequence's token ids as one numpy array (tokens.py:495-511): the view
+    itself for a single mapped part, else one concatenation; never a list."""
+    parts = token_parts(seq)
+    if not parts:
+        return np.empty(0, dtype=np.int32)
+    return parts[0] if len(parts) == 1 else np.concatenate(parts)
+
+
+class ArrowTokenDocuments:
+    """A list<int> Arrow column as documents of TokenViews (tokens.py:103-136)."""
+
+    def __init__(self, array):
+        self._array = array
+        chunks = tuple(array.chunks) if hasattr(array, "chunks") else (array,)
+        self._chunks = chunks
+        self._ends = np.cumsum([len(c) for c in chunks], dtype=np.int64).tolist()
+        self._offsets = tuple(c.offsets.to_numpy(zero_copy_only=True) for c in chunks)
+        self._values = tuple(c.values for c in chunks)
+
+    def __len__(self):
+        return self._ends[-1] if self._ends else 0
+
+    def __getitem__(self, index):
+        if isinstance(index, slice):
+            return [self[i] for i in range(*index.indices(len(self)))]
+        if index < 0:
+            index += len(self)
+        if not 0 <= index < len(self):
+            raise IndexError(index)
+        c = bisect.bisect_right(self._ends, index)
+        local = index - (self._ends[c - 1] if c else 0)
+        start, end = int(self._offsets[c][local]), int(self._offsets[c][local + 1])
+        return TokenView(self._values[c].slice(start, end - start))
+
+
+# ------------------------------------------------------------- on-disk stores
+
+def _pa():
+    import pyarrow as pa
+    return pa
+
+
+class TokenLengths:
+    """A token store's document lengths, read from its count column (tokens.py:139-152)."""
+
+    def __init__(self, store):
+        self._store = store
+
+    def __len__(self):
+        return len(self._store)
+
+    def __getitem__(self, index):
+        if isinstance(index, slice):
+            return [self[i] for i in range(*index.indices(len(self)))]
+        b, local = self._store._locate(index)
+        return int(self._store._counts[b][local])
+
+    def numpy(self):
+        """All lengths as one int64 array."""
+        if not self._store._counts:
+            return np.empty(0, dtype=np.int64)
+        return np.concatenate(self._store._counts).astype(np.int64, copy=False)
+
+
+class _Writer:
+    """One Arrow IPC file written batch by batch; removed again on abort."""
+
+    def __init__(self, path, schema):
+        pa = _pa()
+        self.path = path
+        self._schema = schema
+        self._sink = pa.OSFile(path, "wb")
+        self._ipc = pa.ipc.new_file(self._sink, schema)
+
+    def _write(self, arrays):
+        self._ipc.write_batch(_pa().RecordBatch.from_arrays(arrays, schema=self._schema))
+
+    def _close(self):
+        self._ipc.close()
+        self._sink.close()
+
+    def abort(self):
+        try:
+            self._close()
+        finally:
+            try:
+                os.unlink(self.path)
+            except FileNotFoundError:
+                pass
+
+
+class TokenStoreWriter(_Writer):
+    """Tokenize the document column of source batches into a token store
+    (tokens.py:193-229)."""
+
+    def __init__(self, path, *, document_column, tokenizer, token_type):
+        pa = _pa()
+        self._column = document_column
+        self._tokenizer = tokenizer
+        self._list_type = pa.large_list(token_type)
+        schema = pa.schema(
+            [pa.field(TokenStore.TOKEN_COLUMN, self._list_type, nullable=False),
+             pa.field(TokenStore.COUNT_COLUMN, pa.int64(), nullable=False)],
+            metadata={b"quail.kind": b"token_store"})
+        super().__init__(path, schema)
+
+    def write_tokens(self, documents):
+        """Append one batch of already tokenized documents (sequences of ids)."""
+        pa = _pa()
+        value_type = self._list_type.value_type
+        lengths = np.fromiter((len(d) for d in documents), dtype=np.int64, count=len(documents))
+        offsets = np.zeros(len(documents) + 1, dtype=np.int64)
+        np.cumsum(lengths, out=offsets[1:])
+        parts = [token_array(d) for d in documents]
+        flat = (np.concatenate(parts) if parts else np.empty(0, np.int64)).astype(
+            value_type.to_pandas_dtype(), copy=False)
+        tokens = pa.LargeListArray.from_arrays(pa.array(offsets, pa.int64()),
+                                               pa.array(flat, value_type))
+        self._write([tokens, pa.array(lengths, pa.int64())])
+
+    def write_batch(self, batch):
+        """Tokenize the document column of one source record batch."""
+        texts = batch.column(batch.schema.get_field_index(self._column))
+        self.write_tokens([self._tokenizer(t.as_py()) for t in texts])
+
+    def finish(self):
+        self._close()
+        return TokenStore(self.path)
+
+
+class TokenStore:
+    """Random access to the documents of one memory mapped token store file
+    (tokens.py:296-356)."""
+
+    TOKEN_COLUMN = "__quail_token_ids"
+    COUNT_COLUMN = "__quail_token_count"
+
+    def __init__(self, path):
+        pa = _pa()
+        self.path = path
+        self._source = pa.memory_map(path, "r")
+        self._reader = pa.ipc.open_file(self._source)
+        self._docs, self._counts, self._ends = [], [], []
+        total = 0
+        for b in range(self._reader.num_record_batches):
+            batch = self._reader.get_batch(b)
+            self._docs.append(ArrowTokenDocuments(batch.column(self.TOKEN_COLUMN)))
+            self._counts.append(batch.column(self.COUNT_COLUMN).to_numpy(zero_copy_only=True))
+            total += batch.num_rows
+            self._ends.append(total)
+        self._lengths = TokenLengths(self)
+
+    @classmethod
+    def write(cls, path, batches, *, document_column, tokenizer, token_type):
+        """Tokenize bounded source batches into one file and open it."""
+        return _write_all(TokenStoreWriter(path, document_column=document_column,
+                                           tokenizer=tokenizer, token_type=token_type),
+                          batches, "write_batch")
+
+    @classmethod
+    def from_documents(cls, path, documents, *, token_type=None, batch_rows=4096):
+        """Write already tokenized documents (sequences of ids), `batch_rows` per
+        record batch, and open the file."""
+        token_type = _pa().int32() if token_type is None else token_type
+        writer = TokenStoreWriter(path, document_column=None, tokenizer=None,
+                                  token_type=token_type)
+        batches = [documents[i:i + batch_rows] for i in range(0, len(documents), batch_rows)]
+        return _write_all(writer, batches, "write_tokens")
+
+    @property
+    def lengths(self):
+        return self._lengths
+
+    def _locate(self, index):
+        if index < 0:
+            index += len(self)
+        if not 0 <= index < len(self):
+            raise IndexError(index)
+        b = bisect.bisect_right(self._ends, index)
+        return b, index - (self._ends[b - 1] if b else 0)
+
+    def __len__(self):
+        return self._ends[-1] if self._ends else 0
+
+    def __getitem__(self, index):
+        if isinstance(index, slice):
+            return [self[i] for i in range(*index.indices(len(self)))]
+        b, local = self._locate(index)
+        return self._docs[b][local]
+
+    def select(self, indices):
+        return TokenSelection(self.path, indices)
+
+    def close(self):
+        self._source.close()
+
+
+def _write_all(writer, batches, method):
+    try:
+        for batch in batches:
+            getattr(writer, method)(batch)
+    except BaseException:
+        writer.abort()
+        raise
+    return writer.finish()
+
+
+class ColumnStoreWriter(_Writer):
+    """Copy one source column into a column store file (tokens.py:232-251)."""
+
+    def __init__(self, path, field):
+        pa = _pa()
+        self._name = field.name
+        super().__init__(path, pa.schema([field], metadata={b"quail.kind": b"column_store"}))
+
+    def write_batch(self, batch):
+        self._write([batch.column(batch.schema.get_field_index(self._name))])
+
+    def finish(self):
+        self._close()
+        return ColumnStore(self.path)
+
+
+class ColumnStore:
+    """One memory mapped source column kept for result rows (tokens.py:254-287)."""
+
+    def __init__(self, path):
+        pa = _pa()
+        self.path = path
+        self._source = pa.memory_map(path, "r")
+        self._reader = pa.ipc.open_file(self._source)
+        self.name = self._reader.schema.names[0]
+        self._values = None
+
+    @classmethod
+    def write(cls, path, batches, field):
+        return _write_all(ColumnStoreWriter(path, field), batches, "write_batch")
+
+    @property
+    def values(self):
+        if self._values is None:
+            pa = _pa()
+            self._values = pa.chunked_array(
+                [self._reader.get_batch(i).column(0)
+                 for i in range(self._reader.num_record_batches)],
+                type=self._reader.schema.field(0).type)
+        return self._values
+
+    def __len__(self):
+        return len(self.values)
+
+    def close(self):
+        self._source.close()
+
+
+class TokenSelection:
+    """Selected documents of a token store, opened lazily; pickles as (path,
+    indices) so a child process maps the file itself (tokens.py:384-409)."""
+
+    def __init__(self, path, indices):
+        self._path = path
+        self._indices = indices
+        self._store = None
+
+    def _open(self):
+        if self._store is None:
+            self._store = TokenStore(self._path)
+        return self._store
+
+    def __len__(self):
+        return len(self._indices)
+
+    def __getitem__(self, index):
+        if isinstance(index, slice):
+            return [self[i] for i in range(*index.indices(len(self)))]
+        return self._open()[self._indices[index]]
+
+    def __getstate__(self):
+        return self._path, self._indices
+
+    def __setstate__(self, state):
+        self._path, self._indices = state
+        self._store = None
+
+
+def select_documents(documents, indices):
+    """Selected documents, by file reference for a token store (tokens.py:458-462)."""
+    if isinstance(documents, TokenStore):
+        return documents.select(indices)
+    return [documents[i] for i in indices]

@@ -22,6 +22,7 @@ output). The bars, written in the tests:
 
 from dataclasses import replace
 
+import numpy as np
 import pytest
 import torch
 
@@ -251,6 +252,27 @@ def test_unified_and_tree_paths_agree_on_the_gpu():
     for d in range(len(docs)):
         if a[d] != b[d]:
             assert abs(ma[d]) <= 0.25 and abs(mb[d]) <= 0.25, f"row {d}"
+
+
+@pytest.mark.gpu
+def test_filter_from_a_token_store_matches_in_memory_documents(tmp_path):
+    """The same rows read from a memory-mapped Arrow token store (int32 ids,
+    several record batches) pack the same chunks and give the same answers
+    and margins, bit for bit."""
+    from quail_amd.tokens import TokenStore
+    model = build_random_qwen3(TINY, seed=7, device="cuda", max_pos=2048,
+                               answer_token_ids=TINY_TRUE + TINY_FALSE)
+    docs, tail = tiny_workload(seed=8, n_rows=24)
+    store = TokenStore.from_documents(str(tmp_path / "rows.arrow"), docs, batch_rows=5)
+    a, ma, ra, _ = gpu_filter(model, TINY, docs, tail, path="tree", pages=160,
+                              budget=900, true_ids=TINY_TRUE, false_ids=TINY_FALSE)
+    b, mb, rb, _ = gpu_filter(model, TINY, store, tail, path="tree", pages=160,
+                              budget=900, true_ids=TINY_TRUE, false_ids=TINY_FALSE)
+    assert a == b and ma == mb
+    assert len(ra) == len(rb)
+    for (ha, _, _), (hb, _, _) in zip(ra, rb):
+        assert np.array_equal(ha["input_ids"], hb["input_ids"])
+        assert np.array_equal(ha["positions"], hb["positions"])
 
 
 @pytest.mark.parametrize("path", ["unified", "tree"])
