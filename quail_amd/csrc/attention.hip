@@ -102,6 +102,26 @@ __global__ __launch_bounds__(1024) void attn_tile_scan_kernel(
   if (threadIdx.x == 0) tile_off[n_seqs] = carry;
 }
 
+// The sequence of q-tile b: the largest s in [0, n) with off[s] <= b, where
+// off is non-decreasing and off[0] = 0 <= b. A 64-way search: each round the
+// wave's lanes load 64 evenly spaced candidates at once and a ballot picks
+// the last one <= b, so n <= 4096 takes two dependent loads where a binary
+// search of scalar loads takes twelve (each an L2 round trip, paid before a
+// workgroup can start its first DMA). Every lane of the wave must call it.
+__device__ __forceinline__ int tile_seq(const int32_t* __restrict__ off, int n, int b, int lane) {
+  int lo = 0, span = n;  // off[lo] <= b; the answer lies in [lo, lo + span)
+  while (span > 1) {
+    const int step = (span + 63) >> 6;
+    const int idx = lo + lane * step;
+    const bool ok = lane * step < span && off[idx] <= b;
+    const unsigned long long m = __builtin_amdgcn_ballot_w64(ok);
+    const int k = 63 - __builtin_clzll(m);  // lane 0 always holds (off[lo] <= b)
+    lo += k * step;
+    span = min(step, span - k * step);
+  }
+  return __builtin_amdgcn_readfirstlane(lo);
+}
+
 template <bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
   using namespace attn;
@@ -118,12 +138,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
   const int b = blockIdx.x;
   const int total_tiles = p.tile_off[p.n_seqs];
   if (b >= total_tiles) return;
-  int lo = 0, hi = p.n_seqs - 1;
-  while (lo < hi) {  // largest s with tile_off[s] <= b
-    const int mid = (lo + hi + 1) >> 1;
-    if (p.tile_off[mid] <= b) lo = mid; else hi = mid - 1;
-  }
-  const int s = lo;
+  const int s = tile_seq(p.tile_off, p.n_seqs, b, lane);
   const int q0 = p.cu_q[s];
   const int count = p.cu_q[s + 1] - q0;
   const int n_tiles = (count + BQ - 1) / BQ;
@@ -346,6 +361,31 @@ constexpr int HALF = BKV * D * 2;  // 8 KiB: K or V^T of one tile
 constexpr int STAGE = 2 * HALF;
 }  // namespace pattn
 
+// The fp8 epilogue's store of one wave's 32 x 128 e4m3 block. A lane holds
+// row `col` of the q-tile, bytes d = 32*db + 8*g + 4*half .. +3 in w[db][g];
+// stored straight from there, every 4-byte store touches 32 rows. The block
+// goes through the wave's own padded LDS rows (`stage`, 32 x 144 bytes) and
+// leaves as whole 128-byte rows, 8 rows per 16-byte-per-lane store. Rows at
+// or past `rows` are not written. The caller has ended every wave's use of
+// the LDS area first.
+__device__ __forceinline__ void store_fp8_rows(uint8_t* stage, const uint32_t (&w)[4][4],
+                                               int lane, uint8_t* out, long ld, int rows) {
+  constexpr int ROWB = 144;
+  const int col = lane & 31, half = lane >> 5;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<uint32_t*>(stage + col * ROWB + 32 * db + 8 * g + 4 * half) = w[db][g];
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int row = 8 * k + (lane >> 3), chunk = lane & 7;
+    const uint4 v = *reinterpret_cast<const uint4*>(stage + row * ROWB + 16 * chunk);
+    if (row < rows) *reinterpret_cast<uint4*>(out + row * ld + 16 * chunk) = v;
+  }
+}
+
 __device__ __forceinline__ int kperm(int i) {
   return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
 }
@@ -373,12 +413,7 @@ __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
   const int b = blockIdx.x;
   const int total_tiles = p.tile_off[p.n_seqs];
   if (b >= total_tiles) return;
-  int lo = 0, hi = p.n_seqs - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (p.tile_off[mid] <= b) lo = mid; else hi = mid - 1;
-  }
-  const int s = lo;
+  const int s = tile_seq(p.tile_off, p.n_seqs, b, lane);
   const int q0 = p.cu_q[s];
   const int count = p.cu_q[s + 1] - q0;
   const int n_qt = (count + BQ - 1) / BQ;
@@ -607,18 +642,23 @@ __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
         amax = fmaxf(amax, fabsf(v));
       }
     amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-    if (my_i >= count) return;
     const float scale = group_scale(amax, p.ue8m0 != 0);
-    uint8_t* qp = p.out_q + qi * p.ld_out_q + (long)hq * D;
+    uint32_t w[4][4];
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        uint32_t w = 0;
+        w[db][g] = 0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) w |= quant_e4m3(acc_o[db][4 * g + r], scale) << (8 * r);
-        *reinterpret_cast<uint32_t*>(qp + 32 * db + 8 * g + 4 * half) = w;
+        for (int r = 0; r < 4; ++r) w[db][g] |= quant_e4m3(acc_o[db][4 * g + r], scale) << (8 * r);
       }
+    // every wave is past its last read of the stages (and every DMA landed)
+    // before the stages become staging rows
+    __builtin_amdgcn_s_barrier();
+    store_fp8_rows(lds + wave * 32 * 144, w, lane,
+                   p.out_q + (long)(q0 + i0) * p.ld_out_q + (long)hq * D, p.ld_out_q,
+                   count - i0);
+    if (my_i >= count) return;
     if (half == 0) p.out_scales[(long)hq * p.n_out + qi] = scale;
   } else {
     if (my_i >= count) return;
@@ -713,12 +753,7 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
   const int b = blockIdx.x;
   const int total_tiles = p.tile_off[p.n_seg];
   if (b >= total_tiles) return;
-  int lo = 0, hi = p.n_seg - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (p.tile_off[mid] <= b) lo = mid; else hi = mid - 1;
-  }
-  const int s = lo;
+  const int s = tile_seq(p.tile_off, p.n_seg, b, lane);
   const int q0 = p.cu_a[s];
   const int count = p.cu_a[s + 1] - q0;
   const int n_qt = (count + BQ - 1) / BQ;
@@ -1014,18 +1049,23 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
         amax = fmaxf(amax, fabsf(v));
       }
     amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-    if (my_i >= count) return;
     const float scale = group_scale(amax, p.ue8m0 != 0);
-    uint8_t* qp = p.out_q + qi * p.ld_out_q + (long)hq * D;
+    uint32_t w[4][4];
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        uint32_t w = 0;
+        w[db][g] = 0;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) w |= quant_e4m3(acc_o[db][4 * g + rr], scale) << (8 * rr);
-        *reinterpret_cast<uint32_t*>(qp + 32 * db + 8 * g + 4 * half) = w;
+        for (int rr = 0; rr < 4; ++rr) w[db][g] |= quant_e4m3(acc_o[db][4 * g + rr], scale) << (8 * rr);
       }
+    // every wave is past its last read of the stages (and every DMA landed)
+    // before the stages become staging rows
+    __builtin_amdgcn_s_barrier();
+    store_fp8_rows(lds + wave * 32 * 144, w, lane,
+                   p.out_q + (long)(q0 + i0) * p.ld_out_q + (long)hq * D, p.ld_out_q,
+                   count - i0);
+    if (my_i >= count) return;
     if (half == 0) p.out_scales[(long)hq * p.n_rows + qi] = scale;
   } else {
     if (my_i >= count) return;
