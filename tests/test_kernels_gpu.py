@@ -75,6 +75,22 @@ def test_group_quant_bit_exact(ue8m0):
     assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8))
 
 
+def test_group_quant_division_is_exact_over_wide_magnitudes():
+    """y / scale is formed as y * (1 / scale) in fp64 and rounded once to fp32;
+    it must equal torch's fp32 division everywhere, so 16k groups of values
+    spread over 2^-30 .. 2^30, each group with its own non-power-of-two
+    scale, quantize bit for bit as the oracle does."""
+    g = _gen(21)
+    rows = 4096
+    mag = torch.pow(2.0, torch.randint(-30, 31, (rows, 1), generator=g).float())
+    x = (torch.randn(rows, 512, generator=g) * mag * (1 + torch.rand(rows, 512, generator=g)))
+    x = x.to(torch.bfloat16)
+    q_ref, s_ref = ref.group_quant(x.float())
+    q, s = K.group_quant(x.to(DEV))
+    assert torch.equal(s.cpu(), s_ref)
+    assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8))
+
+
 def test_e4m3_encoding_matches_torch_at_every_midpoint():
     # Rows whose amax is 448 quantize with scale exactly 1, so the kernel's
     # e4m3 encoder sees the raw values: every finite e4m3 value, every
