@@ -260,39 +260,41 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
   // A lane holds 4 consecutive columns of one token per n-tile, so storing
   // straight from registers writes 16 scattered 32-byte pieces per
   // instruction, which measured ~16k cycles per tile. Instead each wave
-  // stages a few rows of its output at a time in its own LDS slice (rows
-  // padded so that the writes are bank-conflict free) and stores whole rows,
-  // 16 bytes per lane. The slice is the wave's activation region, free
+  // stages part of its output at a time in its own LDS slice (rows padded
+  // so that the writes are bank-conflict free) and stores whole 128-byte row
+  // segments, 16 bytes per lane. The slice is the wave's activation region, free
   // between the read of its fragments and the next activation DMA.
   uint8_t* const slice = areg;
   auto store_bf16 = [&](const Cursor& c) __attribute__((always_inline)) {
-    constexpr int ROWB = 512 + 32;  // one 256-column bf16 row + pad
+    // eight passes, one per token half j and column quarter qd (n-tiles
+    // 4qd .. 4qd+3): every lane writes its 4 x 4 columns of row lane % 16
+    // into 16 staged rows of 64 columns (row pitch 144 bytes: each half-wave's
+    // 8-byte writes cover all 64 banks once), then each lane reads back 16
+    // bytes and the wave stores 8 whole 128-byte row segments per instruction
+    constexpr int ROWB = 128 + 16;
     uint8_t* C = (uint8_t*)p.C;
     const long ldc_b = p.ldc * 2;
 #pragma unroll
     for (int pass = 0; pass < 8; ++pass) {
-      // rows 4*pass .. +3 of the wave's 32: token half j = pass / 4, held by
-      // the lanes with (lane % 16) / 4 == pass % 4, row r = lane % 4
-      const int j = pass >> 2;
-      if (((lane & 15) >> 2) == (pass & 3)) {
-        uint8_t* w = slice + (lane & 3) * ROWB + 8 * g;
+      const int j = pass >> 2, qd = pass & 3;
+      uint8_t* w = slice + (lane & 15) * ROWB + 8 * g;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          // v_cvt_pk_bf16_f32: round-to-nearest-even, as f32_to_bf16
-          const bf16x2 p0 = {(__bf16)acc[i][j][0], (__bf16)acc[i][j][1]};
-          const bf16x2 p1 = {(__bf16)acc[i][j][2], (__bf16)acc[i][j][3]};
-          *reinterpret_cast<uint2*>(w + 32 * i) =
-              make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
-        }
+      for (int ii = 0; ii < 4; ++ii) {
+        const int i = 4 * qd + ii;
+        // v_cvt_pk_bf16_f32: round-to-nearest-even, as f32_to_bf16
+        const bf16x2 p0 = {(__bf16)acc[i][j][0], (__bf16)acc[i][j][1]};
+        const bf16x2 p1 = {(__bf16)acc[i][j][2], (__bf16)acc[i][j][3]};
+        *reinterpret_cast<uint2*>(w + 32 * ii) =
+            make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
       }
-      // two rows per instruction: lanes 0-31 row 2q, lanes 32-63 row 2q+1
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int R = 2 * q + (lane >> 5), chunk = lane & 31;
+      for (int k = 0; k < 2; ++k) {
+        const int R = 8 * k + (lane >> 3), chunk = lane & 7;
         const uint4 v = *reinterpret_cast<const uint4*>(slice + R * ROWB + chunk * 16);
-        const int m = c.tm * BM + 32 * wave + 4 * pass + R;
+        const int m = c.tm * BM + 32 * wave + 16 * j + R;
         if (m < M)
-          *reinterpret_cast<uint4*>(C + (long)m * ldc_b + (long)c.tn * BR * 2 + chunk * 16) = v;
+          *reinterpret_cast<uint4*>(C + (long)m * ldc_b + (long)c.tn * BR * 2 + qd * 128 +
+                                    chunk * 16) = v;
       }
     }
 #pragma unroll
