@@ -130,6 +130,21 @@ int qh_qk_norm_rope(const void* qkv, long ld_qkv, const int64_t* positions,
                     void* q_out, void* k_out, void* v_out, qh_stream_t stream);
 
 /*
+ * qh_qk_norm_rope with k and v written straight into the paged arena instead
+ * of k_out/v_out: row t's k and v go to arena row dst[t], for every row
+ * (the unified path writes each chunk row once). Fuses Engine.qk_norm_rope
+ * (attention.py:777-781 -> :361-409) with the unified call's kv_row_scatter
+ * (attention.py:411-427, called at :933-934); q_out, and the arena rows, are
+ * bit-identical to qh_qk_norm_rope followed by qh_kv_row_scatter.
+ *   dst [T] int64 arena rows; pools in the arena layout above.
+ */
+int qh_qk_norm_rope_kv(const void* qkv, long ld_qkv, const int64_t* positions,
+                       const void* cos_sin, int max_pos, const void* qw,
+                       const void* kw, float eps, int T, int n_q, int n_kv, int d,
+                       void* q_out, void* k_pool, void* v_pool, const int64_t* dst,
+                       int page_tokens, qh_stream_t stream);
+
+/*
  * KV append: arena row dst[i] <- chunk row src[i], for K and V.
  * Replaces Triton kv_row_scatter (attention.py:411-427, called at :725-736,
  * :847-848, :933-934). k_src/v_src are [rows, n_kv, d] bf16 contiguous; the

@@ -39,6 +39,8 @@ SIGNATURES = {
                                _i, _p],
     "qh_qk_norm_rope": [_p, _l, _p, _p, _i, _p, _p, _f, _i, _i, _i, _i,
                         _p, _p, _p, _p],
+    "qh_qk_norm_rope_kv": [_p, _l, _p, _p, _i, _p, _p, _f, _i, _i, _i, _i,
+                           _p, _p, _p, _p, _i, _p],
     "qh_kv_row_scatter": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "qh_kv_row_copy": [_p, _p, _p, _p, _i, _i, _i, _i, _p],
     "qh_attention_workspace_bytes": [_i],

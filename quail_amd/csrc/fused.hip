@@ -146,6 +146,55 @@ __global__ __launch_bounds__(256) void silu_mul_quant_kernel(
 // A 16-lane group owns one 128-wide head slot; slot s reads qkv columns
 // s*128.. (q heads, then k heads, then v heads). Lane j < 8 holds the first
 // half's columns 8j..8j+7, lane j >= 8 the matching second-half columns.
+// RMSNorm (weight w) + NeoX RoPE of one 128-wide q or k head, for the 16
+// threads of a group (j = lane % 16 holds elements 8j .. 8j+7); the partner
+// halves (d, d+64) sit in threads j and j^8. Shared by the plain and the
+// KV-writing kernels so both produce the same bits.
+__device__ __forceinline__ bf16x8 norm_rope_head(bf16x8 xv, const uint16_t* __restrict__ wt,
+                                                 const uint16_t* __restrict__ cs_row,
+                                                 float eps, int j) {
+  // sum of squares: the first half's and the second half's, then together
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += xv.get(e) * xv.get(e);
+  ss = group_sum<8>(ss);                     // within each half
+  const float other = __shfl_xor(ss, 8, kWave);
+  const float total_ss = (j < 8) ? ss + other : other + ss;
+  const float rstd = 1.0f / sqrtf(total_ss / 128.0f + eps);
+  bf16x8 wv = load8(wt + j * 8);
+  float n[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) n[e] = xv.get(e) * rstd * wv.get(e);
+  // partner half
+  float p[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(n[e], 8, kWave);
+  const int hc = (j & 7) * 8;
+  bf16x8 cv = load8(cs_row + hc);
+  bf16x8 sv = load8(cs_row + 64 + hc);
+  bf16x8 out;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float c = cv.get(e), s = sv.get(e);
+    float r;
+    if (j < 8) {
+      r = n[e] * c - p[e] * s;   // a' = a cos - b sin
+    } else {
+      r = n[e] * c + p[e] * s;   // b' = b cos + a sin
+    }
+    out.set(e, f32_to_bf16(r));
+  }
+  return out;
+}
+
+__device__ __forceinline__ const uint16_t* cos_sin_row(const uint16_t* __restrict__ cos_sin,
+                                                       const int64_t* __restrict__ positions,
+                                                       int t, int max_pos) {
+  int64_t pos = positions[t];
+  pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
+  return cos_sin + pos * 128;
+}
+
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ qkv, long ld_qkv,
     const int64_t* __restrict__ positions, const uint16_t* __restrict__ cos_sin,
@@ -164,44 +213,75 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     return;
   }
   const bool is_q = slot < n_q;
-  const uint16_t* wt = is_q ? qw : kw;
-  // sum of squares: the first half's and the second half's, then together
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) ss += xv.get(e) * xv.get(e);
-  ss = group_sum<8>(ss);                     // within each half
-  const float other = __shfl_xor(ss, 8, kWave);
-  const float total_ss = (j < 8) ? ss + other : other + ss;
-  const float rstd = 1.0f / sqrtf(total_ss / 128.0f + eps);
-  bf16x8 wv = load8(wt + j * 8);
-  float n[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) n[e] = xv.get(e) * rstd * wv.get(e);
-  // partner half
-  float p[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) p[e] = __shfl_xor(n[e], 8, kWave);
-  int64_t pos = positions[t];
-  pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
-  const int hc = (j & 7) * 8;
-  bf16x8 cv = load8(cos_sin + pos * 128 + hc);
-  bf16x8 sv = load8(cos_sin + pos * 128 + 64 + hc);
-  bf16x8 out;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float c = cv.get(e), s = sv.get(e);
-    float r;
-    if (j < 8) {
-      r = n[e] * c - p[e] * s;   // a' = a cos - b sin
-    } else {
-      r = n[e] * c + p[e] * s;   // b' = b cos + a sin
-    }
-    out.set(e, f32_to_bf16(r));
-  }
+  const bf16x8 out = norm_rope_head(xv, is_q ? qw : kw,
+                                    cos_sin_row(cos_sin, positions, t, max_pos), eps, j);
   if (is_q) {
     store8(q_out + ((long)t * n_q + slot) * 128 + j * 8, out);
   } else {
     store8(k_out + ((long)t * n_kv + (slot - n_q)) * 128 + j * 8, out);
+  }
+}
+
+// qk_norm_rope with k and v written straight into the paged arena: row t's
+// k and v go to arena row dst[t] (the unified path writes every chunk row).
+// One launch, two kinds of workgroup. The first 3 T work as
+// qk_norm_rope_kernel (row t, 16 head slots each, the same per-head
+// arithmetic), writing q to q_out and k into its K page row. The last
+// ceil(T / 16) each take 16 rows' v from qkv, stage them in LDS and write V^T
+// with the row index fastest, as kv_scatter_kernel does.
+constexpr int kRopeRows = 16;
+
+__global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
+    const uint16_t* __restrict__ qkv, long ld_qkv,
+    const int64_t* __restrict__ positions, const uint16_t* __restrict__ cos_sin,
+    int max_pos, const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
+    float eps, int T, int n_q, int n_kv, int slot_blocks, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
+    const int64_t* __restrict__ dst, int page) {
+  extern __shared__ uint16_t vbuf[];  // [row][n_kv * 128 + 2]
+  const long head_blocks = (long)T * slot_blocks;
+  const int j = threadIdx.x & 15;
+  if ((long)blockIdx.x < head_blocks) {
+    const int t = (int)(blockIdx.x / slot_blocks);
+    const int slot = (int)(blockIdx.x % slot_blocks) * 16 + (threadIdx.x >> 4);
+    if (slot >= n_q + n_kv) return;  // v: the row-block workgroups
+    const bf16x8 xv = load8(qkv + (long)t * ld_qkv + (long)slot * 128 + j * 8);
+    const bool is_q = slot < n_q;
+    const bf16x8 out = norm_rope_head(xv, is_q ? qw : kw,
+                                      cos_sin_row(cos_sin, positions, t, max_pos), eps, j);
+    if (is_q) {
+      store8(q_out + ((long)t * n_q + slot) * 128 + j * 8, out);
+    } else {
+      const long r = dst[t];
+      const long pg = r / page, sl = r % page;
+      store8(k_pool + ((pg * n_kv + (slot - n_q)) * page + sl) * 128 + j * 8, out);
+    }
+    return;
+  }
+  const int row_elems = n_kv * 128;
+  const int ld = row_elems + 2;
+  const int t0 = (int)(blockIdx.x - head_blocks) * kRopeRows;
+  const int rows = min(kRopeRows, T - t0);
+  const int chunks = rows * n_kv * 16;  // 16-byte chunks of the rows' v
+  const uint16_t* vsrc = qkv + (long)(n_q + n_kv) * 128;
+  for (int c = threadIdx.x; c < chunks; c += 256) {
+    const int e = c / (n_kv * 16), hc = c % (n_kv * 16);
+    const bf16x8 vv = load8(vsrc + (long)(t0 + e) * ld_qkv + hc * 8);
+    uint32_t* vl = reinterpret_cast<uint32_t*>(vbuf + e * ld + hc * 8);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) vl[w] = vv.w[w];
+  }
+  __syncthreads();
+  // V^T: work item = (head, d, row), row fastest
+  const int items = row_elems * kRopeRows;
+  for (int it = threadIdx.x; it < items; it += 256) {
+    const int e = it & (kRopeRows - 1);
+    if (e >= rows) continue;
+    const int hd = it >> 4;  // h * 128 + d
+    const long r = dst[t0 + e];
+    const long pg = r / page, sl = r % page;
+    const int h = hd >> 7, d = hd & 127;
+    v_pool[((pg * n_kv + h) * 128 + d) * page + sl] = vbuf[e * ld + hd];
   }
 }
 
@@ -486,6 +566,32 @@ extern "C" int qh_qk_norm_rope(const void* qkv, long ld_qkv, const int64_t* posi
                      max_pos, (const uint16_t*)qw, (const uint16_t*)kw, eps, T, n_q,
                      n_kv, (uint16_t*)q_out, (uint16_t*)k_out, (uint16_t*)v_out);
   return launch_status("qk_norm_rope");
+}
+
+extern "C" int qh_qk_norm_rope_kv(const void* qkv, long ld_qkv, const int64_t* positions,
+                                  const void* cos_sin, int max_pos, const void* qw,
+                                  const void* kw, float eps, int T, int n_q, int n_kv, int d,
+                                  void* q_out, void* k_pool, void* v_pool, const int64_t* dst,
+                                  int page_tokens, qh_stream_t stream) {
+  QH_REQUIRE(d == 128, "qk_norm_rope_kv: head_dim %d unsupported (128 only)", d);
+  QH_REQUIRE(n_q > 0 && n_kv > 0 && T >= 0 && max_pos > 0 && page_tokens > 0,
+             "qk_norm_rope_kv: geometry");
+  QH_REQUIRE(n_kv <= 15, "qk_norm_rope_kv: n_kv=%d exceeds the 64 KiB staging buffer", n_kv);
+  QH_REQUIRE(ld_qkv >= (long)(n_q + 2 * n_kv) * d && ld_qkv % 8 == 0,
+             "qk_norm_rope_kv: row stride %ld", ld_qkv);
+  if (T == 0) return QH_OK;
+  QH_REQUIRE(qkv && positions && cos_sin && qw && kw && q_out && k_pool && v_pool && dst,
+             "qk_norm_rope_kv: null pointer");
+  const size_t smem = (size_t)kRopeRows * (n_kv * 128 + 2) * sizeof(uint16_t);
+  const int slot_blocks = blocks_for(n_q + n_kv, 16);
+  const long grid = (long)T * slot_blocks + blocks_for(T, kRopeRows);
+  QH_REQUIRE(grid < 0x7fffffffL, "qk_norm_rope_kv: %d rows exceed the grid", T);
+  hipLaunchKernelGGL(qk_norm_rope_kv_kernel, dim3((unsigned)grid), dim3(256), smem,
+                     (hipStream_t)stream, (const uint16_t*)qkv, ld_qkv, positions,
+                     (const uint16_t*)cos_sin, max_pos, (const uint16_t*)qw,
+                     (const uint16_t*)kw, eps, T, n_q, n_kv, slot_blocks, (uint16_t*)q_out,
+                     (uint16_t*)k_pool, (uint16_t*)v_pool, dst, page_tokens);
+  return launch_status("qk_norm_rope_kv");
 }
 
 extern "C" int qh_kv_row_scatter(const void* k_src, const void* v_src, void* k_pool,

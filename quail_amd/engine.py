@@ -44,11 +44,12 @@ class Engine:
 
     def __init__(self, arena, *, n_q, n_kv, head_dim, rotary, fp8=True,
                  kernels_name="quail", ue8m0=False, gemm_hook=None,
-                 attention_hook=None, tree_kernel="fused"):
+                 attention_hook=None, tree_kernel="fused", fuse_kv_write=True):
         import torch
         if tree_kernel not in ("fused", "two_pass"):
             raise ValueError(f"tree_kernel must be 'fused' or 'two_pass', got {tree_kernel!r}")
         self.tree_kernel = tree_kernel
+        self.fuse_kv_write = bool(fuse_kv_write)
         if not fp8:
             raise ValueError("this build runs fp8 block-scaled linears only")
         if kernels_name != "quail":
@@ -106,6 +107,26 @@ class Engine:
         q, k, _ = self.qkv_norm_rope(qkv, positions, attn)
         return q, k
 
+    def qkv_attention(self, qkv, positions, attn, chunk):
+        """qkv_norm_rope then attention. On the unified path, where every chunk
+        row is written to the arena, the norm/RoPE kernel writes k and v into
+        the layer's pages itself (no k/v rows, no separate scatter); the
+        result is bit-identical to the two-step form."""
+        meta = chunk.meta
+        unified = meta.get("unified")
+        if (self.fuse_kv_write and chunk.attention_mode != "tree" and unified is not None
+                and unified.get("row_dst") is not None):
+            k_pool, v_pool = self.arena.layer_kv(meta["layer"])
+            q = kernels.qk_norm_rope_kv(
+                qkv, positions, self.rotary.cos_sin_cache, attn.q_norm.weight,
+                attn.k_norm.weight, attn.q_norm.variance_epsilon, self.num_q_heads,
+                self.num_kv_heads, self.head_dim, k_pool, v_pool, unified["row_dst"])
+            n = q.shape[0]
+            return self.attention_unified(q.view(n, self.num_q_heads, self.head_dim), None,
+                                          None, meta, n)
+        q, k, v = self.qkv_norm_rope(qkv, positions, attn)
+        return self.attention(q, k, v, chunk)
+
     def fused_add_rms_norm_rows(self, hidden, residual, rows, norm):
         """Final norm of the answer rows: gather + add + RMSNorm in one kernel."""
         return kernels.final_norm(hidden, residual, rows, norm.weight,
@@ -147,7 +168,8 @@ class Engine:
             meta["layer"] += 1
             return self.quant(out.view(n, -1))
         k_pool, v_pool = self.arena.layer_kv(layer)
-        kernels.kv_row_scatter(k3, v3, k_pool, v_pool, unified["src"], unified["dst"])
+        if k3 is not None:  # else the norm/RoPE kernel already wrote the rows
+            kernels.kv_row_scatter(k3, v3, k_pool, v_pool, unified["src"], unified["dst"])
         if unified["tail_src"] is not None:
             kernels.kv_row_copy(k_pool, v_pool, unified["tail_src"], unified["tail_dst"])
         work = meta.get("work", {})

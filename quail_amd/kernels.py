@@ -146,6 +146,26 @@ def qk_norm_rope(qkv, positions, cos_sin, q_weight, k_weight, eps, n_q, n_kv,
     return q, k, v
 
 
+def qk_norm_rope_kv(qkv, positions, cos_sin, q_weight, k_weight, eps, n_q, n_kv,
+                    head_dim, k_pool, v_pool, row_dst, page_tokens=PAGE_TOKENS):
+    """qk_norm_rope with row t's k and v written to arena row row_dst[t]
+    (the Triton qk_norm_rope, attention.py:361-409, then the unified call's
+    kv_row_scatter, :411-427, in one pass). Returns q."""
+    _check(qkv, torch.bfloat16, "qkv", dim=2)
+    _check(cos_sin, torch.bfloat16, "cos_sin", dim=2)
+    if positions.dtype != torch.int64 or not positions.is_contiguous():
+        raise ValueError("positions must be contiguous int64")
+    T = qkv.shape[0]
+    if row_dst.dtype != torch.int64 or row_dst.numel() != T or not row_dst.is_contiguous():
+        raise ValueError("row_dst must be contiguous int64, one arena row per chunk row")
+    q = torch.empty((T, n_q * head_dim), dtype=torch.bfloat16, device=qkv.device)
+    _hip.call("qh_qk_norm_rope_kv", _ptr(qkv), qkv.stride(0), _ptr(positions),
+              _ptr(cos_sin), cos_sin.shape[0], _ptr(q_weight), _ptr(k_weight),
+              float(eps), T, n_q, n_kv, head_dim, _ptr(q), _ptr(k_pool), _ptr(v_pool),
+              _ptr(row_dst), page_tokens, _stream())
+    return q
+
+
 def kv_row_scatter(k_rows, v_rows, k_pool, v_pool, src, dst,
                    page_tokens=PAGE_TOKENS):
     """Arena rows dst[i] <- chunk rows src[i] (attention.py:411-427)."""

@@ -313,12 +313,21 @@ def pack_chunk(torch, arena, groups, timing=None, pinned=True, *, attention_mode
             for key in temporary_keys:
                 arena.free_key(key)
             raise
-        arrays.update(unified_src=_cat(src), unified_dst=_cat(dst),
+        usrc, udst = _cat(src), _cat(dst)
+        arrays.update(unified_src=usrc, unified_dst=udst,
                       unified_used=np.asarray(lengths, dtype=np.int32),
                       unified_table=arena.block_table_np(page_rows),
                       unified_cu_q=np.asarray(ucu, dtype=np.int32))
         if tail_src:
             arrays.update(tail_src=_cat(tail_src), tail_dst=_cat(tail_dst))
+        # the arena row of every chunk row, when the scatter writes each row
+        # exactly once (it does: every group's rows are emitted once): lets
+        # the q/k norm + RoPE kernel write k and v into the arena itself
+        if usrc.size == token_count:
+            row_dst = np.full(token_count, -1, dtype=np.int64)
+            row_dst[usrc] = udst
+            if (row_dst >= 0).all():
+                arrays["unified_row_dst"] = row_dst
         unified_host = dict(max_used=max(lengths),
                             max_q=max(b - a for a, b in zip(ucu, ucu[1:])))
 
@@ -350,6 +359,7 @@ def pack_chunk(torch, arena, groups, timing=None, pinned=True, *, attention_mode
     unified = None
     if unified_host is not None:
         unified = dict(src=staged["unified_src"], dst=staged["unified_dst"],
+                       row_dst=staged.get("unified_row_dst"),
                        tail_src=staged.get("tail_src"), tail_dst=staged.get("tail_dst"),
                        used=staged["unified_used"], table=staged["unified_table"],
                        cu_q=staged["unified_cu_q"], **unified_host)

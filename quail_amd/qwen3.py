@@ -33,7 +33,7 @@ class Qwen3Pipeline(ModelPipeline):
 
     def __init__(self, model, arena, *, spec=None, kernels_name="quail",
                  engine_class=Engine, ue8m0=False, gemm_hook=None, attention_hook=None,
-                 tree_kernel="fused"):
+                 tree_kernel="fused", fuse_kv_write=True):
         import torch
         self.layers = model.model.layers
         self.embed = model.model.embed_tokens
@@ -44,7 +44,7 @@ class Qwen3Pipeline(ModelPipeline):
                                    head_dim=attn.head_dim, rotary=attn.rotary_emb,
                                    fp8=fp8, kernels_name=kernels_name, ue8m0=ue8m0,
                                    gemm_hook=gemm_hook, attention_hook=attention_hook,
-                                   tree_kernel=tree_kernel)
+                                   tree_kernel=tree_kernel, fuse_kv_write=fuse_kv_write)
         self.tree_attention = fp8
         widest = max(max(layer.self_attn.qkv_proj.weight.shape[0],
                          layer.mlp.gate_up_proj.weight.shape[0]) for layer in self.layers)
@@ -76,8 +76,7 @@ class Qwen3Pipeline(ModelPipeline):
             else:
                 q_in, q_scale = engine.norm_quant(hidden, layer.input_layernorm, residual)
             qkv = engine.gemm(q_in, q_scale, attn.qkv_proj, "qkv")
-            q, k, v = engine.qkv_norm_rope(qkv, positions, attn)
-            o_in, o_scale = engine.attention(q, k, v, chunk)
+            o_in, o_scale = engine.qkv_attention(qkv, positions, attn, chunk)
             hidden = engine.gemm(o_in, o_scale, attn.o_proj, "o")
             g_in, g_scale = engine.norm_quant(hidden, layer.post_attention_layernorm,
                                               residual)

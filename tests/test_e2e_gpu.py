@@ -254,6 +254,31 @@ def test_unified_and_tree_paths_agree_on_the_gpu():
             assert abs(ma[d]) <= 0.25 and abs(mb[d]) <= 0.25, f"row {d}"
 
 
+def test_fused_kv_write_gives_the_same_answers():
+    """The unified path with q/k norm + RoPE writing k and v into the arena
+    itself answers every row with the same margins, bit for bit, as with the
+    separate k/v rows and scatter."""
+    model = build_random_qwen3(TINY, seed=9, device="cuda", max_pos=2048,
+                               answer_token_ids=TINY_TRUE + TINY_FALSE)
+    docs, tail = tiny_workload(seed=10, n_rows=24)
+    runs = []
+    for fuse in (False, True):
+        arena = KVArena(len(model.model.layers), 160, 16, TINY.n_kv, TINY.d_head,
+                        dtype=torch.bfloat16, device="cuda")
+        pipe = Qwen3Pipeline(model, arena, spec=TINY, fuse_kv_write=fuse)
+        rows = AnswerRows(torch, model, TINY_TRUE, TINY_FALSE)
+        ans = AsyncAnswers(torch, rows, keep_margins=True)
+        stream = loop.FilterStream(torch, arena, pipe, ans, docs, [list(tail)], 900,
+                                   arena_writes=True, attention_mode="unified",
+                                   prefix_tree=prefix_tree(docs, 16))
+        while not stream.done:
+            stream.next()
+        torch.cuda.synchronize()
+        runs.append(([stream.answers[d][0] for d in range(len(docs))],
+                     [float(m) for ms in ans.margins for m in ms]))
+    assert runs[0] == runs[1]
+
+
 @pytest.mark.gpu
 def test_filter_from_a_token_store_matches_in_memory_documents(tmp_path):
     """The same rows read from a memory-mapped Arrow token store (int32 ids,

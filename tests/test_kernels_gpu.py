@@ -387,6 +387,39 @@ def test_merge_attn_quant():
     _check_quant(q, s, q_ref, s_ref, max_frac_off=1e-3, scale_rtol=0)
 
 
+def test_qk_norm_rope_kv_equals_rope_then_scatter():
+    """q, and the arena rows the fused kernel writes k and v into, are bit for
+    bit qk_norm_rope followed by kv_row_scatter; 83 rows (a ragged last block
+    of 16), arena rows in runs starting mid-page plus scattered singles, every
+    other arena row untouched."""
+    g = _gen(51)
+    T, n_q, n_kv, d = 83, 32, 8, 128
+    n_pages = 40
+    qkv = torch.randn(T, (n_q + 2 * n_kv) * d, generator=g).to(torch.bfloat16)
+    pos = torch.randint(0, 4000, (T,), generator=g)
+    cs = ref.rope_cache(4096, d, 1e6)
+    qw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    kw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    run = torch.cat([torch.arange(9 * 16 + 5, 11 * 16), torch.arange(3 * 16, 4 * 16)])
+    rest = torch.tensor([r for r in torch.randperm(n_pages * 16, generator=g).tolist()
+                         if r not in set(run.tolist())][:T - run.numel()])
+    row_dst = torch.cat([run, rest]).to(torch.int64)
+    base_k = torch.randn(n_pages * 16, n_kv, d, generator=g).to(torch.bfloat16)
+    base_v = torch.randn(n_pages * 16, n_kv, d, generator=g).to(torch.bfloat16)
+    args = (qkv.to(DEV), pos.to(DEV), cs.to(DEV), qw.to(DEV), kw.to(DEV), 1e-6, n_q, n_kv, d)
+    q_a, k_a, v_a = K.qk_norm_rope(*args)
+    kp_a = layout.k_pool_from_rows(base_k).to(DEV)
+    vp_a = layout.v_pool_from_rows(base_v).to(DEV)
+    K.kv_row_scatter(k_a.view(T, n_kv, d), v_a.view(T, n_kv, d), kp_a, vp_a,
+                     torch.arange(T, device=DEV), row_dst.to(DEV))
+    kp_b = layout.k_pool_from_rows(base_k).to(DEV)
+    vp_b = layout.v_pool_from_rows(base_v).to(DEV)
+    q_b = K.qk_norm_rope_kv(*args, kp_b, vp_b, row_dst.to(DEV))
+    assert torch.equal(q_b.view(torch.int16), q_a.view(torch.int16))
+    assert torch.equal(kp_b.view(torch.int16), kp_a.view(torch.int16))
+    assert torch.equal(vp_b.view(torch.int16), vp_a.view(torch.int16))
+
+
 def test_kv_row_scatter_and_copy_bit_exact():
     g = _gen(50)
     n_pages, n_kv, d = 24, 8, 128
