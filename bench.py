@@ -238,7 +238,7 @@ def main():
     ap.add_argument("--attention", default=None, choices=["unified", "tree"],
                     help="default: unified for filters, tree for the join")
     ap.add_argument("--arena-pages", type=int, default=None)
-    ap.add_argument("--cpu-rows", type=int, default=2)
+    ap.add_argument("--cpu-rows", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
