@@ -313,8 +313,9 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     results = []
+    host = {}   # host-side phases of the loop (admission, allocation, packing, ...)
     for _ in range(args.steps):
-        answers, stats = runner.run(instruction, documents, tail)
+        answers, stats = runner.run(instruction, documents, tail, timing=host)
         results.append((answers, stats))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -394,6 +395,8 @@ def main():
                       "gather_frac_hbm": round(k["attn_gbps"] / HBM_PEAK_GBPS, 4),
                       "share_of_step": round(k["attn_ms"] / (ms_per_step * args.steps), 3),
                       "calls": k["attn_kinds"]},
+        "host_ms_per_step": {k: round(1e3 * v / args.steps, 1) for k, v in host.items()
+                             if k != "n_chunks"},
         "answers_true": int(sum(answers)), "deterministic_across_steps": steady,
         "build_s": round(build_s, 1),
         "cpu_baseline": cpu,
