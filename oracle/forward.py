@@ -17,32 +17,40 @@ from oracle import ops
 class OracleArena:
     """Per-layer logical K/V pools, arena rows page * 16 + slot."""
 
-    def __init__(self, n_layers, n_pages, n_kv, head_dim, page_tokens=16):
+    def __init__(self, n_layers, n_pages, n_kv, head_dim, page_tokens=16, device="cpu"):
         rows = n_pages * page_tokens
-        self.k = [torch.zeros(rows, n_kv, head_dim, dtype=torch.bfloat16)
+        self.k = [torch.zeros(rows, n_kv, head_dim, dtype=torch.bfloat16, device=device)
                   for _ in range(n_layers)]
-        self.v = [torch.zeros(rows, n_kv, head_dim, dtype=torch.bfloat16)
+        self.v = [torch.zeros(rows, n_kv, head_dim, dtype=torch.bfloat16, device=device)
                   for _ in range(n_layers)]
 
 
 def cpu_weights(model):
     """CPU copies of a quail_amd.model model's tensors, in a flat dict."""
+    return oracle_weights(model, "cpu")
+
+
+def oracle_weights(model, device):
+    """A quail_amd.model model's tensors on `device`, in a flat dict. The
+    oracle only reads them; on the model's own device they are the model's
+    tensors themselves."""
     inner = model.model
-    w = {"embed": inner.embed_tokens.weight.cpu(), "final_norm": inner.norm.weight.cpu(),
+    to = lambda x: x.to(device)
+    w = {"embed": to(inner.embed_tokens.weight), "final_norm": to(inner.norm.weight),
          "final_eps": inner.norm.variance_epsilon,
-         "cos_sin": model.rotary.cos_sin_cache.cpu(),
-         "answer": model.quail_answer_weights.cpu(),
+         "cos_sin": to(model.rotary.cos_sin_cache),
+         "answer": to(model.quail_answer_weights),
          "answer_ids": model.quail_answer_token_ids, "layers": []}
     for layer in inner.layers:
         a, m = layer.self_attn, layer.mlp
         w["layers"].append(dict(
-            qkv=(a.qkv_proj.weight.cpu(), a.qkv_proj.weight_scale.cpu()),
-            o=(a.o_proj.weight.cpu(), a.o_proj.weight_scale.cpu()),
-            gate_up=(m.gate_up_proj.weight.cpu(), m.gate_up_proj.weight_scale.cpu()),
-            down=(m.down_proj.weight.cpu(), m.down_proj.weight_scale.cpu()),
-            q_norm=a.q_norm.weight.cpu(), k_norm=a.k_norm.weight.cpu(),
-            in_norm=layer.input_layernorm.weight.cpu(),
-            post_norm=layer.post_attention_layernorm.weight.cpu(),
+            qkv=(to(a.qkv_proj.weight), to(a.qkv_proj.weight_scale)),
+            o=(to(a.o_proj.weight), to(a.o_proj.weight_scale)),
+            gate_up=(to(m.gate_up_proj.weight), to(m.gate_up_proj.weight_scale)),
+            down=(to(m.down_proj.weight), to(m.down_proj.weight_scale)),
+            q_norm=to(a.q_norm.weight), k_norm=to(a.k_norm.weight),
+            in_norm=to(layer.input_layernorm.weight),
+            post_norm=to(layer.post_attention_layernorm.weight),
             eps=layer.input_layernorm.variance_epsilon, cos_sin=w["cos_sin"],
             n_q=a.num_heads, n_kv=a.num_kv_heads, head_dim=a.head_dim))
     return w
@@ -106,8 +114,9 @@ def forward_chunk(w, host, attention_mode, arena, gemm=exact_gemm, ue8m0=False,
 
 
 def _forward(w, host, attention_mode, arena, gemm, quant, ue8m0, page_tokens):
-    ids = torch.from_numpy(host["input_ids"])
-    finals = torch.from_numpy(host["finals"])
+    dev = w["embed"].device
+    ids = torch.from_numpy(host["input_ids"]).to(dev)
+    finals = torch.from_numpy(host["finals"]).to(dev)
     hidden = w["embed"][ids]
     residual = None
     for li, L in enumerate(w["layers"]):
@@ -123,8 +132,8 @@ def layer_step(L, li, hidden, residual, host, attention_mode, arena, gemm=exact_
     """One Qwen3 decoder layer (models/qwen3.py:55-71): (hidden, residual) in,
     (down-projection output, residual) out; residual None at layer 0.
     Writes the layer's KV into arena.k[li] / arena.v[li] as the chunk says."""
-    t = lambda name: torch.from_numpy(host[name])
-    pos = t("positions")
+    t = lambda name: torch.from_numpy(host[name])   # host side; ops move what they index with
+    pos = t("positions").to(hidden.device)
     T = pos.numel()
     n_q, n_kv, d, eps = L["n_q"], L["n_kv"], L["head_dim"], L["eps"]
     if residual is None:
@@ -157,7 +166,7 @@ def layer_step(L, li, hidden, residual, host, attention_mode, arena, gemm=exact_
         if "unified_src" in host:
             ops.kv_row_scatter(kp, vp, k3, v3, t("unified_src"), t("unified_dst"))
             if "tail_src" in host:
-                src, dst = t("tail_src"), t("tail_dst")
+                src, dst = t("tail_src").to(kp.device), t("tail_dst").to(kp.device)
                 kp[dst] = kp[src]
                 vp[dst] = vp[src]
             out, _ = ops.paged_attention(q3, kp, vp, t("unified_cu_q"), t("unified_used"),

@@ -192,7 +192,7 @@ def fp8_gemm(a_q, a_scales, w_q, w_scales, out_dtype=torch.bfloat16):
     a = a_q.double().view(M, kb_n, GROUP)
     w = w_q.double().view(N, kb_n, GROUP)
     sb = w_scales.double().repeat_interleave(GROUP, dim=0)  # [N, kb]
-    out = torch.zeros(M, N, dtype=torch.float64)
+    out = torch.zeros(M, N, dtype=torch.float64, device=a_q.device)
     for kb in range(kb_n):
         part = a[:, kb, :] @ w[:, kb, :].T
         out += part * a_scales[:, kb].double()[:, None] * sb[:, kb][None, :]
@@ -215,7 +215,7 @@ def fp8_gemm_blockwise_fp32(a_q, a_scales, w_q, w_scales, out_dtype=torch.bfloat
     a = a_q.double().view(M, kb_n, GROUP)
     w = w_q.double().view(N, kb_n, GROUP)
     sb = w_scales.float().repeat_interleave(GROUP, dim=0)   # [N, kb]
-    acc = torch.zeros(M, N, dtype=torch.float32)
+    acc = torch.zeros(M, N, dtype=torch.float32, device=a_q.device)
     for kb in range(kb_n):
         block = (a[:, kb, :] @ w[:, kb, :].T).float()
         s = a_scales[:, kb].float()[:, None] * sb[:, kb][None, :]
@@ -246,13 +246,13 @@ def attend(q, k, v, scale, visible):
     return out, lse
 
 
-def causal_visible(c, kv_len):
+def causal_visible(c, kv_len, device="cpu"):
     """Bottom-right aligned causal mask: query i of c sees keys 0..kv_len-c+i.
 
     The alignment tests/kv_checker.py:132-139 asserts for the paged call.
     """
-    i = torch.arange(c)[:, None]
-    j = torch.arange(kv_len)[None, :]
+    i = torch.arange(c, device=device)[:, None]
+    j = torch.arange(kv_len, device=device)[None, :]
     return j <= (kv_len - c + i)
 
 
@@ -263,8 +263,8 @@ def gather_pages(pool, table_row, kv_len, page=PAGE):
     table_row[j // page] * page + j % page (arena.py:519-523, :874-887).
     """
     j = torch.arange(kv_len)
-    rows = table_row[j // page].long() * page + j % page
-    return pool[rows]
+    rows = table_row.cpu()[j // page].long() * page + j % page
+    return pool[rows.to(pool.device)]
 
 
 def paged_attention(q3, k_pool, v_pool, cu_q, used, table, scale, causal,
@@ -279,19 +279,20 @@ def paged_attention(q3, k_pool, v_pool, cu_q, used, table, scale, causal,
     used = [int(x) for x in used]
     n_queries = cu_q[-1]
     H, d = q3.shape[1], q3.shape[2]
-    out = torch.zeros(n_queries, H, d)
-    lse = torch.full((H, n_queries), float("-inf"))
+    dev = q3.device
+    out = torch.zeros(n_queries, H, d, device=dev)
+    lse = torch.full((H, n_queries), float("-inf"), device=dev)
     for s in range(len(used)):
         a, b = cu_q[s], cu_q[s + 1]
         c = b - a
         if c == 0:
             continue
         rows = torch.arange(a, b) if q_rows is None else q_rows[a:b].long()
-        q = q3[rows]
+        q = q3[rows.to(dev)]
         k = gather_pages(k_pool, table[s], used[s], page)
         v = gather_pages(v_pool, table[s], used[s], page)
-        vis = (causal_visible(c, used[s]) if causal
-               else torch.ones(c, used[s], dtype=torch.bool))
+        vis = (causal_visible(c, used[s], dev) if causal
+               else torch.ones(c, used[s], dtype=torch.bool, device=dev))
         o, l = attend(q, k, v, scale, vis)
         out[a:b] = o
         lse[:, a:b] = l
@@ -305,15 +306,16 @@ def varlen_attention(q3, k3, v3, cu, scale, causal=True):
     """
     cu = [int(x) for x in cu]
     T, H, d = q3.shape
-    out = torch.zeros(T, H, d)
-    lse = torch.full((H, T), float("-inf"))
+    dev = q3.device
+    out = torch.zeros(T, H, d, device=dev)
+    lse = torch.full((H, T), float("-inf"), device=dev)
     for s in range(len(cu) - 1):
         a, b = cu[s], cu[s + 1]
         c = b - a
         if c == 0:
             continue
-        vis = (causal_visible(c, c) if causal
-               else torch.ones(c, c, dtype=torch.bool))
+        vis = (causal_visible(c, c, dev) if causal
+               else torch.ones(c, c, dtype=torch.bool, device=dev))
         o, l = attend(q3[a:b], k3[a:b], v3[a:b], scale, vis)
         out[a:b] = o
         lse[:, a:b] = l
@@ -332,19 +334,20 @@ def tree_attention(q3, k3, v3, cu_a, seg_read, k_pool, v_pool, table, used, scal
     """
     cu = [int(x) for x in cu_a]
     T, H, d = q3.shape
-    out = torch.zeros(T, H, d)
+    dev = q3.device
+    out = torch.zeros(T, H, d, device=dev)
     for s in range(len(cu) - 1):
         a, b = cu[s], cu[s + 1]
         c = b - a
         if c == 0:
             continue
         r = int(seg_read[s])
-        own_vis = causal_visible(c, c)
+        own_vis = causal_visible(c, c, dev)
         if r >= 0:
             n = int(used[r])
             k = torch.cat([gather_pages(k_pool, table[r], n, page).float(), k3[a:b].float()])
             v = torch.cat([gather_pages(v_pool, table[r], n, page).float(), v3[a:b].float()])
-            vis = torch.cat([torch.ones(c, n, dtype=torch.bool), own_vis], dim=1)
+            vis = torch.cat([torch.ones(c, n, dtype=torch.bool, device=dev), own_vis], dim=1)
         else:
             k, v, vis = k3[a:b], v3[a:b], own_vis
         out[a:b], _ = attend(q3[a:b], k, v, scale, vis)
@@ -359,7 +362,7 @@ def merge_attn(out_a, lse_a, out_b, lse_b, source):
     Returns fp32 values of the bf16 result.
     """
     a = out_a.float()
-    src = source.long()
+    src = source.long().to(a.device)
     has_b = src >= 0
     safe = src.clamp(min=0)
     b = out_b.float()[safe]
@@ -380,8 +383,9 @@ def merge_attn_quant(out_a, lse_a, out_b, lse_b, source, ue8m0=False):
 
 def kv_row_scatter(k_pool, v_pool, k_rows, v_rows, src, dst):
     """pool[dst[i]] = rows[src[i]] for K and V (attention.py:415-427), in place."""
-    k_pool[dst.long()] = k_rows[src.long()]
-    v_pool[dst.long()] = v_rows[src.long()]
+    src, dst = src.long().to(k_pool.device), dst.long().to(k_pool.device)
+    k_pool[dst] = k_rows[src]
+    v_pool[dst] = v_rows[src]
 
 
 def answer_bits(normed, w_ans, true_cols, false_cols):

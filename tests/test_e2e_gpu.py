@@ -381,3 +381,70 @@ def test_join_decisions_agree_outside_the_noise_band(path):
                 assert abs(mr) <= 0.25, f"decision differs at margin {mr:.4f}"
     assert total >= 8 * 12 and agree >= 0.95 * total, f"{agree}/{total}"
     print(f"join {path}: GPU-vs-oracle {agree}/{total} final rows")
+
+
+def test_qwen3_4b_decisions_agree_with_the_oracle_within_its_noise():
+    """Full Qwen3-4B geometry (36 layers, random init) over the first 192
+    rows of the seeded 4096-row filter workload, unified path, four chunks.
+    The oracle replays every chunk on the GPU (the same torch functions the
+    CPU runs, on device tensors) twice: with fp64 block sums and with
+    dequantize-then-fp32 GEMMs. The two are equally valid restatements, so
+    their disagreement measures how well posed the decisions are.
+
+    They are not well posed: 36 layers of dynamic 1x128 fp8 re-quantization
+    amplify a one-ulp difference until the two oracles disagree on about
+    one row in eight, with margin shifts as large as the median margin
+    (scaling the layers' residual writes down by 10x does not change
+    that). So the bars are that every row the GPU decides differently
+    from the fp64 oracle lies inside twice the oracles' largest margin
+    shift, and that the GPU agrees with it as often as the other oracle
+    does, within three binomial standard deviations of the two counts."""
+    from quail_amd.aiif import synthetic_filter_workload
+    from quail_amd.model import SYNTHETIC_FALSE_IDS, SYNTHETIC_TRUE_IDS
+    from quail_amd.specs import QWEN3_4B_FP8
+
+    spec = QWEN3_4B_FP8
+    n = 192
+    model = build_random_qwen3(spec, seed=0, device="cuda", max_pos=2048)
+    instruction, documents, tail = synthetic_filter_workload(4096, seed=0, vocab=spec.vocab)
+    docs = [np.concatenate([instruction, d]) for d in documents[:n]]
+    pages = sum(-(-(len(d) + len(tail)) // 16) for d in docs) + 64
+    answers, margins, records, stream = gpu_filter(
+        model, spec, docs, tail, path="unified", pages=pages, budget=16384,
+        true_ids=SYNTHETIC_TRUE_IDS, false_ids=SYNTHETIC_FALSE_IDS)
+    assert len(records) >= 3
+    print(f"{len(records)} chunks, {sum(len(r[0]['positions']) for r in records)} tokens",
+          flush=True)
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    w = oforward.oracle_weights(model, "cuda")
+    runs = {}
+    for name, gemm in (("fp64", oforward.exact_gemm), ("fp32", oforward.DequantGemm())):
+        arena = oforward.OracleArena(spec.layers, pages, spec.n_kv, spec.d_head, device="cuda")
+        bits, marg = {}, {}
+        with torch.no_grad():
+            for (host, mode, _), groups in zip(records, stream.packed_groups):
+                normed = oforward.forward_chunk(w, host, mode, arena, gemm=gemm)
+                b, m = oforward.readout(w, normed, SYNTHETIC_TRUE_IDS, SYNTHETIC_FALSE_IDS)
+                for (doc, _, _), x, y in zip(groups, b.tolist(), m.tolist()):
+                    bits[doc], marg[doc] = x, y
+        runs[name] = (bits, marg)
+        del arena
+        torch.cuda.empty_cache()
+    (ref_bits, ref_m), (alt_bits, alt_m) = runs["fp64"], runs["fp32"]
+    shift = max(abs(ref_m[d] - alt_m[d]) for d in range(n))
+    band = 2 * shift
+    floor = sum(ref_bits[d] == alt_bits[d] for d in range(n))
+    agree = sum(answers[d] == ref_bits[d] for d in range(n))
+    gpu_shift = max(abs(margins[d] - ref_m[d]) for d in range(n))
+    typical = float(np.median([abs(ref_m[d]) for d in range(n)]))
+    print(f"GPU-vs-oracle {agree}/{n}, oracle-vs-oracle {floor}/{n}; largest margin shift "
+          f"oracle-vs-oracle {shift:.4f}, GPU-vs-oracle {gpu_shift:.4f}; median |margin| "
+          f"{typical:.4f}", flush=True)
+    for d in range(n):
+        if answers[d] != ref_bits[d]:
+            assert abs(ref_m[d]) <= band, \
+                f"row {d}: decision differs at margin {ref_m[d]:.4f} (noise band {band:.4f})"
+    q = 1.0 - floor / n
+    slack = 3.0 * (2.0 * n * q * (1.0 - q)) ** 0.5
+    assert agree >= floor - slack, f"GPU agrees on {agree}/{n}, the oracles on {floor}/{n}"
