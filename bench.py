@@ -104,7 +104,7 @@ class KernelClock:
             attn_gbps=a_bytes / a_ms / 1e6 if a_ms else 0.0)
 
 
-def cpu_baseline(model, spec, instruction, documents, tail, rows, threads):
+def cpu_baseline(model, spec, instruction, documents, tail, rows, threads, ue8m0=False):
     """The CPU oracle forward over a bounded sample of rows (the first `rows`)."""
     import numpy as np
     import torch
@@ -132,7 +132,7 @@ def cpu_baseline(model, spec, instruction, documents, tail, rows, threads):
     chunk = loop.pack_chunk(torch, arena, groups, attention_mode="unified")
     oarena = oforward.OracleArena(spec.layers, pages, spec.n_kv, spec.d_head)
     t0 = time.perf_counter()
-    normed = oforward.forward_chunk(w, chunk.host, "unified", oarena, gemm=gemm)
+    normed = oforward.forward_chunk(w, chunk.host, "unified", oarena, gemm=gemm, ue8m0=ue8m0)
     bits, margins = oforward.readout(w, normed, SYNTHETIC_TRUE_IDS, SYNTHETIC_FALSE_IDS)
     wall = time.perf_counter() - t0
     return dict(rows_per_s=rows / wall, tok_per_s=chunk.tokens / wall, wall_s=wall,
@@ -239,6 +239,9 @@ def main():
                     help="default: unified for filters, tree for the join")
     ap.add_argument("--arena-pages", type=int, default=None)
     ap.add_argument("--cpu-rows", type=int, default=8)
+    ap.add_argument("--ue8m0", action="store_true",
+                    help="power-of-two (UE8M0) activation and weight scales, applied by the "
+                         "MFMA: the reference's DeepGEMM UE8M0 mode (aiif-4b, gemm-c2)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -281,7 +284,7 @@ def main():
     spec = base if args.layers is None else replace(base, layers=args.layers)
     t_build = time.perf_counter()
     model = build_random_qwen3(spec, seed=args.seed, device="cuda",
-                               max_pos=8192 if big else 2048)
+                               max_pos=8192 if big else 2048, ue8m0=args.ue8m0)
     if big:
         instruction, documents, tail = synthetic_filter_workload(
             args.rows, prefix_tokens=128, uniform_lengths=(1024, 4096), seed=args.seed,
@@ -303,7 +306,7 @@ def main():
     clock.n_q, clock.d, clock.n_kv = spec.n_q, spec.d_head, spec.n_kv
     runner = FilterRunner(model, spec, device_spec=MI355X, n_pages=args.arena_pages,
                           attention_mode=args.attention, gemm_hook=clock.gemm_hook,
-                          attention_hook=clock.attention_hook)
+                          attention_hook=clock.attention_hook, ue8m0=args.ue8m0)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t_build
 
@@ -339,7 +342,7 @@ def main():
         threads = min(16, len(os.sched_getaffinity(0)))
         try:
             base = cpu_baseline(model, spec, instruction, documents, tail, args.cpu_rows,
-                                threads)
+                                threads, ue8m0=args.ue8m0)
             agree = sum(int(b == a) for b, a in zip(base["bits"], answers[:args.cpu_rows]))
             cpu = {"value": round(base["rows_per_s"], 4), "unit": "rows/s",
                    "cores": threads, "kind": "port",
@@ -371,7 +374,9 @@ def main():
                                       "(median 180, cap 1024)")
                        + f", 24-token tail, {args.attention} attention, "
                        + ("rows read from a memory-mapped Arrow token store"
-                          if args.documents == "token-store" else "rows in memory")),
+                          if args.documents == "token-store" else "rows in memory")
+                       + (", UE8M0 scales applied by the MFMA" if args.ue8m0
+                          else ", fp32 block scales")),
                    "rows": args.rows, "layers": spec.layers,
                    "fresh_tokens": stats["fresh_tokens"],
                    "input_tokens": stats["input_tokens"], "chunks": stats.get("chunks"),
@@ -430,15 +435,17 @@ def gemm_bench(args):
     x = torch.randn(M, 9728, generator=g)
     for name, N, Kd in GEMM_SHAPES:
         w = torch.randn(N, Kd, generator=g) * 0.02
-        wq, ws = oops.quantize_weight_blocks(w)
-        xq, xs = oops.group_quant(x[:, :Kd])
+        wq, ws = oops.quantize_weight_blocks(w, ue8m0=args.ue8m0)
+        xq, xs = oops.group_quant(x[:, :Kd], ue8m0=args.ue8m0)
         a = xq.to("cuda")
         sa = K.col_major_scales(M, Kd, "cuda")
         sa.copy_(xs.to("cuda"))
         wq, ws = wq.to("cuda"), ws.to("cuda")
-        variants = [("bf16 out", lambda: K.fp8_gemm_nt(a, sa, wq, ws))]
+        hw = bool(args.ue8m0)
+        variants = [("bf16 out", lambda: K.fp8_gemm_nt(a, sa, wq, ws, ue8m0_scales=hw))]
         if name == "gate_up":
-            variants.append(("silu+fp8 out", lambda: K.fp8_gemm_silu_quant(a, sa, wq, ws)))
+            variants.append(("silu+fp8 out", lambda: K.fp8_gemm_silu_quant(
+                a, sa, wq, ws, ue8m0=hw, ue8m0_scales=hw)))
         flops = 2.0 * M * N * Kd
         rec = {}
         for label, fn in variants:
@@ -459,7 +466,7 @@ def gemm_bench(args):
         total_ms += rec["bf16 out"]["ms"]
         # parity on a row sample: the oracle's exact block sums
         rows = torch.arange(0, M, M // 64)
-        got = K.fp8_gemm_nt(a, sa, wq, ws)[rows.to("cuda")].float().cpu()
+        got = K.fp8_gemm_nt(a, sa, wq, ws, ue8m0_scales=hw)[rows.to("cuda")].float().cpu()
         want = oops.fp8_gemm(xq[rows], xs[rows].contiguous(), wq.cpu(), ws.cpu()).float()
         rec["rel_l2_vs_oracle_64_rows"] = round(((got - want).norm() / want.norm()).item(), 6)
         shapes[name] = dict(N=N, K=Kd, gflop=round(flops / 1e9, 1), **rec)
@@ -489,7 +496,9 @@ def gemm_bench(args):
         "data": "synthetic",
         "config": {"workload": "fp8 block-scaled GEMM sweep, M = 16384, (N, K) in "
                                "{(6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728)}, "
-                               "fp32 128x128 weight / 1x128 activation scales, bf16 out"},
+                               + ("UE8M0 (power-of-two) 128x128 weight / 1x128 activation "
+                                  "scales applied by the MFMA, bf16 out" if args.ue8m0 else
+                                  "fp32 128x128 weight / 1x128 activation scales, bf16 out")},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": FP8_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP8_PEAK_TFLOPS, 4),
                      "traffic": None, "kernel": "qh fp8_gemm_kernel"},

@@ -95,6 +95,20 @@ int qh_fp8_gemm_nt(const void* A, long lda, const float* sa, const void* B,
                    int K, qh_stream_t stream);
 
 /*
+ * qh_fp8_gemm_nt for UE8M0 scales: every sa and sb value is a power of two
+ * (2^-126 .. 2^127), as the reference's scales are when
+ * is_deep_gemm_e8m0_used() holds (attention.py:115, :129-141; vLLM then
+ * rounds the weight block scales up to powers of two at load time and
+ * per_token_group_quant_fp8 runs with use_ue8m0). The MFMA applies the
+ * scales through its own E8M0 operands and accumulates the K blocks in
+ * place; a scale that is not a power of two is read as its power-of-two
+ * exponent alone. Same operands, layouts and limits as qh_fp8_gemm_nt.
+ */
+int qh_fp8_gemm_nt_ue8m0(const void* A, long lda, const float* sa, const void* B,
+                         long ldb, const float* sb, void* C, long ldc, int M, int N,
+                         int K, qh_stream_t stream);
+
+/*
  * The gate_up projection fused with the SiLU-gated product and its 1x128 fp8
  * quantization: replaces Engine.gemm(gate_up_proj) followed by
  * Engine.activation_quant (models/qwen3.py:113-116 -> attention.py:129-141,
@@ -112,6 +126,16 @@ int qh_fp8_gemm_silu_quant(const void* A, long lda, const float* sa,
                            const void* B, long ldb, const float* sb, int M,
                            int I, int K, void* out_q, long ld_out,
                            float* scales, int ue8m0, qh_stream_t stream);
+
+/*
+ * qh_fp8_gemm_silu_quant with UE8M0 input scales (as qh_fp8_gemm_nt_ue8m0)
+ * and UE8M0 output scales (its ue8m0 = 1): the gate_up projection of the
+ * reference's UE8M0 mode (attention.py:115, :300-323).
+ */
+int qh_fp8_gemm_silu_quant_ue8m0(const void* A, long lda, const float* sa,
+                                 const void* B, long ldb, const float* sb, int M,
+                                 int I, int K, void* out_q, long ld_out,
+                                 float* scales, qh_stream_t stream);
 
 /*
  * Per-head RMSNorm of q and k, then NeoX rotary on the two 64-column halves,

@@ -35,8 +35,11 @@ SIGNATURES = {
     "qh_add_rmsnorm_quant": [_p, _l, _p, _l, _p, _f, _i, _i, _p, _p, _i, _p],
     "qh_group_quant": [_p, _l, _i, _i, _p, _p, _i, _p],
     "qh_fp8_gemm_nt": [_p, _l, _p, _p, _l, _p, _p, _l, _i, _i, _i, _p],
+    "qh_fp8_gemm_nt_ue8m0": [_p, _l, _p, _p, _l, _p, _p, _l, _i, _i, _i, _p],
     "qh_fp8_gemm_silu_quant": [_p, _l, _p, _p, _l, _p, _i, _i, _i, _p, _l, _p,
                                _i, _p],
+    "qh_fp8_gemm_silu_quant_ue8m0": [_p, _l, _p, _p, _l, _p, _i, _i, _i, _p, _l, _p,
+                                     _p],
     "qh_qk_norm_rope": [_p, _l, _p, _p, _i, _p, _p, _f, _i, _i, _i, _i,
                         _p, _p, _p, _p],
     "qh_qk_norm_rope_kv": [_p, _l, _p, _p, _i, _p, _p, _f, _i, _i, _i, _i,

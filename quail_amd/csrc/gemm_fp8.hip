@@ -98,7 +98,11 @@ __device__ __forceinline__ float silu_mul_bf16(float gate_acc, float up_acc) {
   return silu_mul(round_bf16(gate_acc), round_bf16(up_acc));
 }
 
-template <int EPI>
+// HW: the activation and weight scales are UE8M0 (powers of two). The MFMA
+// then applies them itself through its E8M0 scale operands and accumulates
+// across K blocks in place, with no promotion FMAs: the exponent byte of an
+// fp32 power of two 2^e is e + 127, which is the E8M0 encoding of 2^e.
+template <int EPI, bool HW>
 __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
   using namespace gemm;
   // weight stages, then one activation region per wave (160 KiB in all)
@@ -412,10 +416,13 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
     const ALoad Ls = a_args(ca);
     const int dstage = (s + NS - 1) % NS;
     float sc[2][2];  // [token half][weight half]
+    int ea[2], eb[2];  // E8M0 exponents (HW): token half, weight half
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       sc[j][0] = sav[slot][j] * sbv[slot][0];
       sc[j][1] = sav[slot][j] * sbv[slot][1];
+      ea[j] = (int)((__builtin_bit_cast(uint32_t, sav[slot][j]) >> 23) & 0xffu);
+      eb[j] = (int)((__builtin_bit_cast(uint32_t, sbv[slot][j]) >> 23) & 0xffu);
     }
     const uint8_t* st = lds + (s % NS) * STAGE;
     const uint8_t* st_next = lds + ((s + 1) % NS) * STAGE;
@@ -427,22 +434,27 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
       const v8i bnn = i < 14 ? frag(st, i + 2) : frag(st_next, i - 14);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const f32x4 t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-            bf, xa[j], zero, 0, 0, 0, 127, 0, 127);
-        // promote the product two MFMAs back: its MFMA finished while the
-        // one in between ran, so the FMAs co-issue with the MFMA pipe
-        // instead of waiting on it (one MFMA back, they wait)
-        const int q = 2 * i + j - 2;
-        if (q >= 0) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[q >> 1][q & 1][r] += tp0[r] * sc[q & 1][(q >> 1) >> 3];
+        if constexpr (HW) {
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              bf, xa[j], acc[i][j], 0, 0, 0, eb[i >> 3], 0, ea[j]);
         } else {
-          const float sl = q == -2 ? s_last0 : s_last1;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[15][q + 2][r] += tp0[r] * sl;
+          const f32x4 t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              bf, xa[j], zero, 0, 0, 0, 127, 0, 127);
+          // promote the product two MFMAs back: its MFMA finished while the
+          // one in between ran, so the FMAs co-issue with the MFMA pipe
+          // instead of waiting on it (one MFMA back, they wait)
+          const int q = 2 * i + j - 2;
+          if (q >= 0) {
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) acc[q >> 1][q & 1][r] += tp0[r] * sc[q & 1][(q >> 1) >> 3];
+          } else {
+            const float sl = q == -2 ? s_last0 : s_last1;
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) acc[15][q + 2][r] += tp0[r] * sl;
+          }
+          tp0 = tp1;
+          tp1 = t;
         }
-        tp0 = tp1;
-        tp1 = t;
       }
       // the step's twelve loads, one per n-tile: activation DMA for step
       // s+1, weight DMA for step s+3, then scales for step s+2
@@ -455,11 +467,17 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
       // two back, MFMA, FMAs. Left alone, the scheduler puts both MFMAs
       // last and their products' FMAs first in the next group, where they
       // wait for the MFMAs instead of running beside them.
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      if constexpr (HW) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     s_last0 = sc[0][1];
@@ -470,13 +488,15 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
     xa0 = frag(areg, 0);
     xa1 = frag(areg, 1);
     if (cc.kb == nk - 1) {
+      if constexpr (!HW) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        acc[15][0][r] += tp0[r] * s_last0;
-        acc[15][1][r] += tp1[r] * s_last1;
+        for (int r = 0; r < 4; ++r) {
+          acc[15][0][r] += tp0[r] * s_last0;
+          acc[15][1][r] += tp1[r] * s_last1;
+        }
+        tp0 = tp1 = zero;
+        s_last0 = s_last1 = 0.f;
       }
-      tp0 = tp1 = zero;
-      s_last0 = s_last1 = 0.f;
       // the region is free once the fragments are in VGPRs
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       epilogue(cc);
@@ -518,13 +538,14 @@ static int device_cus() {
 // activation blocks once per wave of tile columns. group_m = 4 (4 x 8 tiles)
 // was the measured best or within 2 % of it among 1/2/4/8/16 for every
 // Qwen3-4B projection at 102,400 tokens, the fused gate_up included.
-template <int EPI>
+template <int EPI, bool HW = false>
 static int launch_gemm(GemmArgs a, qh_stream_t stream, const char* what) {
   const int tiles_n = a.N / gemm::BR;
   const int tiles = ((a.M + gemm::BM - 1) / gemm::BM) * tiles_n;
   const int grid = min(tiles, device_cus());
   a.group_m = 4;
-  hipLaunchKernelGGL(fp8_gemm_kernel<EPI>, dim3(grid), dim3(512), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL((fp8_gemm_kernel<EPI, HW>), dim3(grid), dim3(512), 0, (hipStream_t)stream,
+                     a);
   return launch_status(what);
 }
 
@@ -538,38 +559,67 @@ static bool offsets_fit(int M, int N, int K, long lda, long ldb) {
 
 using namespace qh;
 
+static int gemm_nt(const void* A, long lda, const float* sa, const void* B, long ldb,
+                   const float* sb, void* C, long ldc, int M, int N, int K, bool hw,
+                   qh_stream_t stream, const char* what) {
+  QH_REQUIRE(M >= 0 && N > 0 && K > 0, "%s: M=%d N=%d K=%d", what, M, N, K);
+  QH_REQUIRE(N % gemm::BR == 0, "%s: N=%d must be a multiple of 256", what, N);
+  QH_REQUIRE(K % gemm::BK == 0, "%s: K=%d must be a multiple of 128", what, K);
+  QH_REQUIRE(lda >= K && ldb >= K && ldc >= N, "%s: leading dimensions", what);
+  QH_REQUIRE(lda % 16 == 0 && ldb % 16 == 0 && ldc % 4 == 0,
+             "%s: lda/ldb must be multiples of 16 bytes, ldc of 4 elements", what);
+  QH_REQUIRE(offsets_fit(M, N, K, lda, ldb), "%s: operands exceed 2 GiB offsets", what);
+  if (M == 0) return QH_OK;
+  QH_REQUIRE(A && sa && B && sb && C, "%s: null pointer", what);
+  GemmArgs a{(const uint8_t*)A, lda, sa, (const uint8_t*)B, ldb, sb, C, ldc, nullptr,
+             M, N, K, 0, 0};
+  return hw ? launch_gemm<gemm::kStoreBf16, true>(a, stream, what)
+            : launch_gemm<gemm::kStoreBf16, false>(a, stream, what);
+}
+
+static int gemm_silu_quant(const void* A, long lda, const float* sa, const void* B, long ldb,
+                           const float* sb, int M, int I, int K, void* out_q, long ld_out,
+                           float* scales, int ue8m0, bool hw, qh_stream_t stream,
+                           const char* what) {
+  QH_REQUIRE(M >= 0 && I > 0 && K > 0, "%s: M=%d I=%d K=%d", what, M, I, K);
+  QH_REQUIRE(I % 128 == 0, "%s: I=%d must be a multiple of 128", what, I);
+  QH_REQUIRE(K % gemm::BK == 0, "%s: K=%d must be a multiple of 128", what, K);
+  QH_REQUIRE(lda >= K && ldb >= K && ld_out >= I, "%s: leading dimensions", what);
+  QH_REQUIRE(lda % 16 == 0 && ldb % 16 == 0 && ld_out % 4 == 0,
+             "%s: lda/ldb must be multiples of 16 bytes, ld_out of 4", what);
+  QH_REQUIRE(offsets_fit(M, 2 * I, K, lda, ldb), "%s: operands exceed 2 GiB offsets", what);
+  if (M == 0) return QH_OK;
+  QH_REQUIRE(A && sa && B && sb && out_q && scales, "%s: null pointer", what);
+  GemmArgs a{(const uint8_t*)A, lda, sa, (const uint8_t*)B, ldb, sb, out_q, ld_out, scales,
+             M, 2 * I, K, ue8m0, 0};
+  return hw ? launch_gemm<gemm::kSiluQuant, true>(a, stream, what)
+            : launch_gemm<gemm::kSiluQuant, false>(a, stream, what);
+}
+
 extern "C" int qh_fp8_gemm_nt(const void* A, long lda, const float* sa, const void* B,
                               long ldb, const float* sb, void* C, long ldc, int M, int N,
                               int K, qh_stream_t stream) {
-  QH_REQUIRE(M >= 0 && N > 0 && K > 0, "fp8_gemm_nt: M=%d N=%d K=%d", M, N, K);
-  QH_REQUIRE(N % gemm::BR == 0, "fp8_gemm_nt: N=%d must be a multiple of 256", N);
-  QH_REQUIRE(K % gemm::BK == 0, "fp8_gemm_nt: K=%d must be a multiple of 128", K);
-  QH_REQUIRE(lda >= K && ldb >= K && ldc >= N, "fp8_gemm_nt: leading dimensions");
-  QH_REQUIRE(lda % 16 == 0 && ldb % 16 == 0 && ldc % 4 == 0,
-             "fp8_gemm_nt: lda/ldb must be multiples of 16 bytes, ldc of 4 elements");
-  QH_REQUIRE(offsets_fit(M, N, K, lda, ldb), "fp8_gemm_nt: operands exceed 2 GiB offsets");
-  if (M == 0) return QH_OK;
-  QH_REQUIRE(A && sa && B && sb && C, "fp8_gemm_nt: null pointer");
-  GemmArgs a{(const uint8_t*)A, lda, sa, (const uint8_t*)B, ldb, sb, C, ldc, nullptr,
-             M, N, K, 0, 0};
-  return launch_gemm<gemm::kStoreBf16>(a, stream, "fp8_gemm_nt");
+  return gemm_nt(A, lda, sa, B, ldb, sb, C, ldc, M, N, K, false, stream, "fp8_gemm_nt");
+}
+
+extern "C" int qh_fp8_gemm_nt_ue8m0(const void* A, long lda, const float* sa, const void* B,
+                                    long ldb, const float* sb, void* C, long ldc, int M,
+                                    int N, int K, qh_stream_t stream) {
+  return gemm_nt(A, lda, sa, B, ldb, sb, C, ldc, M, N, K, true, stream, "fp8_gemm_nt_ue8m0");
 }
 
 extern "C" int qh_fp8_gemm_silu_quant(const void* A, long lda, const float* sa,
                                       const void* B, long ldb, const float* sb, int M,
                                       int I, int K, void* out_q, long ld_out,
                                       float* scales, int ue8m0, qh_stream_t stream) {
-  QH_REQUIRE(M >= 0 && I > 0 && K > 0, "fp8_gemm_silu_quant: M=%d I=%d K=%d", M, I, K);
-  QH_REQUIRE(I % 128 == 0, "fp8_gemm_silu_quant: I=%d must be a multiple of 128", I);
-  QH_REQUIRE(K % gemm::BK == 0, "fp8_gemm_silu_quant: K=%d must be a multiple of 128", K);
-  QH_REQUIRE(lda >= K && ldb >= K && ld_out >= I, "fp8_gemm_silu_quant: leading dimensions");
-  QH_REQUIRE(lda % 16 == 0 && ldb % 16 == 0 && ld_out % 4 == 0,
-             "fp8_gemm_silu_quant: lda/ldb must be multiples of 16 bytes, ld_out of 4");
-  QH_REQUIRE(offsets_fit(M, 2 * I, K, lda, ldb),
-             "fp8_gemm_silu_quant: operands exceed 2 GiB offsets");
-  if (M == 0) return QH_OK;
-  QH_REQUIRE(A && sa && B && sb && out_q && scales, "fp8_gemm_silu_quant: null pointer");
-  GemmArgs a{(const uint8_t*)A, lda, sa, (const uint8_t*)B, ldb, sb, out_q, ld_out, scales,
-             M, 2 * I, K, ue8m0, 0};
-  return launch_gemm<gemm::kSiluQuant>(a, stream, "fp8_gemm_silu_quant");
+  return gemm_silu_quant(A, lda, sa, B, ldb, sb, M, I, K, out_q, ld_out, scales, ue8m0, false,
+                         stream, "fp8_gemm_silu_quant");
+}
+
+extern "C" int qh_fp8_gemm_silu_quant_ue8m0(const void* A, long lda, const float* sa,
+                                            const void* B, long ldb, const float* sb, int M,
+                                            int I, int K, void* out_q, long ld_out,
+                                            float* scales, qh_stream_t stream) {
+  return gemm_silu_quant(A, lda, sa, B, ldb, sb, M, I, K, out_q, ld_out, scales, 1, true,
+                         stream, "fp8_gemm_silu_quant_ue8m0");
 }

@@ -68,9 +68,24 @@ class Engine:
 
     # ---- weights and quant ------------------------------------------
 
+    def hw_scales(self, linear):
+        """Whether this linear's GEMMs hand their scales to the MFMA: UE8M0
+        mode, and weight block scales that are all powers of two (as vLLM
+        leaves them when DeepGEMM runs with UE8M0). Decided once per linear."""
+        if not self.use_ue8m0:
+            return False
+        flag = getattr(linear, "quail_ue8m0_scales", None)
+        if flag is None:
+            mant, _ = self.torch.frexp(linear.weight_scale)
+            flag = bool((mant == 0.5).all().item())
+            linear.quail_ue8m0_scales = flag
+        return flag
+
     def gemm(self, q_input, input_scale, linear, name="gemm"):
         w = linear.weight
-        launch = lambda: kernels.fp8_gemm_nt(q_input, input_scale, w, linear.weight_scale)
+        hw = self.hw_scales(linear)
+        launch = lambda: kernels.fp8_gemm_nt(q_input, input_scale, w, linear.weight_scale,
+                                             ue8m0_scales=hw)
         if self.gemm_hook is not None:
             return self.gemm_hook(name, q_input.shape[0], w.shape[0], w.shape[1], launch)
         return launch()
@@ -79,8 +94,10 @@ class Engine:
         """gate_up GEMM + SiLU gate + fp8 quant in one kernel (gemm then
         activation_quant, bit-identical)."""
         w = linear.weight
+        hw = self.hw_scales(linear)
         launch = lambda: kernels.fp8_gemm_silu_quant(q_input, input_scale, w,
-                                                     linear.weight_scale, self.use_ue8m0)
+                                                     linear.weight_scale, self.use_ue8m0,
+                                                     ue8m0_scales=hw)
         if self.gemm_hook is not None:
             return self.gemm_hook(name, q_input.shape[0], w.shape[0], w.shape[1], launch)
         return launch()

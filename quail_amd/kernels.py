@@ -89,27 +89,31 @@ def _check_gemm(a, a_scales, w, w_scales):
     return M, N, K
 
 
-def fp8_gemm_nt(a, a_scales, w, w_scales, out=None):
+def fp8_gemm_nt(a, a_scales, w, w_scales, out=None, ue8m0_scales=False):
     """out = (a * a_scales) (w * w_scales)^T in bf16 (DeepGEMM fp8_gemm_nt semantics).
 
     a [M, K] e4m3 with (M, K/128) column-major fp32 scales; w [N, K] e4m3
-    with (N/128, K/128) fp32 block scales.
+    with (N/128, K/128) fp32 block scales. ue8m0_scales: every scale of both
+    operands is a power of two, and the MFMA applies them itself
+    (qh_fp8_gemm_nt_ue8m0).
     """
     M, N, K = _check_gemm(a, a_scales, w, w_scales)
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
-    _hip.call("qh_fp8_gemm_nt", _ptr(a), a.stride(0), _ptr(a_scales), _ptr(w),
-              w.stride(0), _ptr(w_scales), _ptr(out), out.stride(0), M, N, K,
-              _stream())
+    _hip.call("qh_fp8_gemm_nt_ue8m0" if ue8m0_scales else "qh_fp8_gemm_nt", _ptr(a),
+              a.stride(0), _ptr(a_scales), _ptr(w), w.stride(0), _ptr(w_scales), _ptr(out),
+              out.stride(0), M, N, K, _stream())
     return out
 
 
-def fp8_gemm_silu_quant(a, a_scales, w, w_scales, ue8m0=False):
+def fp8_gemm_silu_quant(a, a_scales, w, w_scales, ue8m0=False, ue8m0_scales=False):
     """silu_mul_quant(fp8_gemm_nt(a, w)) in one kernel, bit-identical to the pair.
 
     w is the merged gate_up weight [2I, K] (gate rows, then up rows) with
     (2I/128, K/128) block scales. Returns the e4m3 [M, I] activation and its
     (M, I/128) column-major scales (attention.py:300-323 semantics).
+    ue8m0_scales: the input scales are powers of two, applied by the MFMA,
+    and the output scales are UE8M0 too (qh_fp8_gemm_silu_quant_ue8m0).
     """
     M, N, K = _check_gemm(a, a_scales, w, w_scales)
     if N % (2 * GROUP):
@@ -117,9 +121,14 @@ def fp8_gemm_silu_quant(a, a_scales, w, w_scales, ue8m0=False):
     inter = N // 2
     q = torch.empty((M, inter), dtype=torch.float8_e4m3fn, device=a.device)
     scales = col_major_scales(M, inter, a.device)
-    _hip.call("qh_fp8_gemm_silu_quant", _ptr(a), a.stride(0), _ptr(a_scales), _ptr(w),
-              w.stride(0), _ptr(w_scales), M, inter, K, _ptr(q), q.stride(0),
-              _ptr(scales), int(bool(ue8m0)), _stream())
+    if ue8m0_scales:
+        _hip.call("qh_fp8_gemm_silu_quant_ue8m0", _ptr(a), a.stride(0), _ptr(a_scales),
+                  _ptr(w), w.stride(0), _ptr(w_scales), M, inter, K, _ptr(q), q.stride(0),
+                  _ptr(scales), _stream())
+    else:
+        _hip.call("qh_fp8_gemm_silu_quant", _ptr(a), a.stride(0), _ptr(a_scales), _ptr(w),
+                  w.stride(0), _ptr(w_scales), M, inter, K, _ptr(q), q.stride(0),
+                  _ptr(scales), int(bool(ue8m0)), _stream())
     return q, scales
 
 

@@ -22,19 +22,23 @@ SYNTHETIC_FALSE_IDS = (2469, 3557, 4195, 5183)
 INIT_STD = 0.02
 
 
-def _block_quant(torch, w, block=128):
-    """fp32 [N, K] -> (e4m3 [N, K], fp32 [N/128, K/128]), scale = max(amax,1e-10)/448."""
+def _block_quant(torch, w, block=128, ue8m0=False):
+    """fp32 [N, K] -> (e4m3 [N, K], fp32 [N/128, K/128]), scale = max(amax,1e-10)/448,
+    rounded up to a power of two with ue8m0 (vLLM's requantization of the
+    weight scales when DeepGEMM runs in UE8M0 mode)."""
     N, K = w.shape
     b = w.view(N // block, block, K // block, block)
     amax = b.abs().amax(dim=(1, 3))
     scale = amax.clamp(min=1e-10) / 448.0
+    if ue8m0:
+        scale = torch.exp2(torch.ceil(torch.log2(scale)))
     q = (b / scale[:, None, :, None]).clamp(-448.0, 448.0)
     return q.reshape(N, K).to(torch.float8_e4m3fn), scale.contiguous()
 
 
-def _linear(torch, gen, n_out, n_in, device):
+def _linear(torch, gen, n_out, n_in, device, ue8m0=False):
     w = torch.randn(n_out, n_in, generator=gen, device=device, dtype=torch.float32) * INIT_STD
-    q, s = _block_quant(torch, w)
+    q, s = _block_quant(torch, w, ue8m0=ue8m0)
     return SimpleNamespace(weight=q, weight_scale=s, weight_scale_inv=s)
 
 
@@ -53,11 +57,12 @@ def rope_cache(torch, max_pos, head_dim, theta, device):
 
 
 def build_random_qwen3(spec, *, seed=0, device="cuda", layers=None, max_pos=8192,
-                       answer_token_ids=None):
+                       answer_token_ids=None, ue8m0=False):
     """A random-init Qwen3-architecture fp8 model of `spec`'s geometry.
 
     layers overrides spec.layers (tests use shallow models). The same seed
     gives the same weights on any device with the same torch RNG stream.
+    ue8m0: power-of-two weight block scales (the UE8M0 mode's weights).
     """
     import torch
     n_layers = spec.layers if layers is None else layers
@@ -74,13 +79,13 @@ def build_random_qwen3(spec, *, seed=0, device="cuda", layers=None, max_pos=8192
     inner.layers = []
     for _ in range(n_layers):
         attn = SimpleNamespace(
-            qkv_proj=_linear(torch, gen, spec.qkv_width, H, device),
-            o_proj=_linear(torch, gen, H, spec.n_q * d, device),
+            qkv_proj=_linear(torch, gen, spec.qkv_width, H, device, ue8m0),
+            o_proj=_linear(torch, gen, H, spec.n_q * d, device, ue8m0),
             q_norm=_norm(torch, d, eps, device), k_norm=_norm(torch, d, eps, device),
             num_heads=spec.n_q, num_kv_heads=spec.n_kv, head_dim=d, rotary_emb=rotary)
         mlp = SimpleNamespace(
-            gate_up_proj=_linear(torch, gen, spec.ffn_width, H, device),
-            down_proj=_linear(torch, gen, H, spec.intermediate, device))
+            gate_up_proj=_linear(torch, gen, spec.ffn_width, H, device, ue8m0),
+            down_proj=_linear(torch, gen, H, spec.intermediate, device, ue8m0))
         inner.layers.append(SimpleNamespace(
             self_attn=attn, mlp=mlp, input_layernorm=_norm(torch, H, eps, device),
             post_attention_layernorm=_norm(torch, H, eps, device)))

@@ -41,10 +41,11 @@ class Recorder:
         return normed
 
 
-def gpu_filter(model, spec, docs, tail, *, path, pages, budget, true_ids, false_ids):
+def gpu_filter(model, spec, docs, tail, *, path, pages, budget, true_ids, false_ids,
+               ue8m0=False):
     arena = KVArena(len(model.model.layers), pages, 16, spec.n_kv, spec.d_head,
                     dtype=torch.bfloat16, device="cuda")
-    pipe = Recorder(Qwen3Pipeline(model, arena, spec=spec))
+    pipe = Recorder(Qwen3Pipeline(model, arena, spec=spec, ue8m0=ue8m0))
     rows = AnswerRows(torch, model, true_ids, false_ids)
     ans = AsyncAnswers(torch, rows, keep_margins=True)
     stream = loop.FilterStream(torch, arena, pipe, ans, docs, [list(tail)], budget,

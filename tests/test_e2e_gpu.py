@@ -178,6 +178,40 @@ def test_decisions_agree_outside_the_noise_band(path):
           f"largest oracle-vs-oracle margin shift {shift:.4f}")
 
 
+def test_ue8m0_mode_runs_the_mfma_scaled_gemms_and_agrees_with_the_oracle():
+    """UE8M0 mode end to end: power-of-two weight block scales and UE8M0
+    activation quantization, so every GEMM runs with the MFMA applying the
+    scales (qh_fp8_gemm_nt_ue8m0, qh_fp8_gemm_silu_quant_ue8m0). The oracle
+    replays the chunks in UE8M0 mode; decisions agree outside the noise band
+    as in fp32-scale mode."""
+    model = build_random_qwen3(TINY, seed=5, device="cuda", max_pos=2048,
+                               answer_token_ids=TINY_TRUE + TINY_FALSE, ue8m0=True)
+    docs, tail = tiny_workload(seed=6, n_rows=64)
+    pages = 300
+    answers, margins, records, stream = gpu_filter(
+        model, TINY, docs, tail, path="unified", pages=pages, budget=2000,
+        true_ids=TINY_TRUE, false_ids=TINY_FALSE, ue8m0=True)
+    layer = model.model.layers[0]
+    for lin in (layer.self_attn.qkv_proj, layer.self_attn.o_proj, layer.mlp.gate_up_proj,
+                layer.mlp.down_proj):
+        assert getattr(lin, "quail_ue8m0_scales", False) is True
+    w = oforward.cpu_weights(model)
+    arena = oforward.OracleArena(TINY.layers, pages, TINY.n_kv, TINY.d_head)
+    ref_bits, ref_m = {}, {}
+    for (host, mode, _), groups in zip(records, stream.packed_groups):
+        normed = oforward.forward_chunk(w, host, mode, arena, ue8m0=True)
+        b, m = oforward.readout(w, normed, TINY_TRUE, TINY_FALSE)
+        for (doc, _, _), x, y in zip(groups, b.tolist(), m.tolist()):
+            ref_bits[doc], ref_m[doc] = x, y
+    n = len(docs)
+    agree = sum(answers[d] == ref_bits[d] for d in range(n))
+    for d in range(n):
+        if answers[d] != ref_bits[d]:
+            assert abs(ref_m[d]) <= 0.25, f"row {d}: decision differs at margin {ref_m[d]:.4f}"
+    assert agree >= 0.95 * n, f"GPU agrees on {agree}/{n}"
+    print(f"ue8m0: GPU-vs-oracle {agree}/{n}")
+
+
 def test_each_layer_stage_matches_the_oracle_on_identical_inputs():
     import math
     from oracle import ops

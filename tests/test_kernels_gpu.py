@@ -216,6 +216,60 @@ def test_fp8_gemm_silu_quant_matches_pair(M, I, Kd, ue8m0):
     assert torch.equal(q.view(torch.uint8).cpu(), q_pair.view(torch.uint8).cpu())
 
 
+def _ue8m0_inputs(seed, M, N, Kd):
+    """UE8M0-quantized weights N(0, 0.02) and activations N(0, 1) (CPU), with
+    the activation scales also on the GPU in the column-major layout."""
+    g = _gen(seed)
+    wq, ws = ref.quantize_weight_blocks(torch.randn(N, Kd, generator=g) * 0.02, ue8m0=True)
+    xq, xs = ref.group_quant(torch.randn(M, Kd, generator=g), ue8m0=True)
+    mant_w, _ = torch.frexp(ws)
+    mant_x, _ = torch.frexp(xs)
+    assert (mant_w == 0.5).all() and (mant_x == 0.5).all()
+    xs_dev = K.col_major_scales(M, Kd, DEV)
+    xs_dev.copy_(xs)
+    return xq, xs, xs_dev, wq, ws
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 256, 128), (300, 512, 2560), (517, 6144, 2560),
+                                    (2333, 19456, 384), (256, 2560, 9728)])
+def test_fp8_gemm_nt_ue8m0_matches_the_oracle(M, N, Kd):
+    """UE8M0 scales applied by the MFMA's E8M0 operands: against the oracle's
+    fp64 block sums (same bar as the fp32-scale kernel), and against the
+    fp32-promotion kernel on the same operands, which computes the same sums
+    with power-of-two (exact) promotion multipliers."""
+    xq, xs, xs_dev, wq, ws = _ue8m0_inputs(30 + M, M, N, Kd)
+    want = ref.fp8_gemm(xq, xs, wq, ws, out_dtype=torch.float64)
+    got = K.fp8_gemm_nt(xq.to(DEV), xs_dev, wq.to(DEV), ws.to(DEV), ue8m0_scales=True)
+    err = (got.cpu().double() - want).abs()
+    tol = want.abs() * 2 ** -8 + 1e-3 * want.abs().max()
+    assert (err <= tol).all(), f"max err {err.max().item()} (scale {want.abs().max().item()})"
+    promo = K.fp8_gemm_nt(xq.to(DEV), xs_dev, wq.to(DEV), ws.to(DEV)).float()
+    rel = ((got.float() - promo).norm() / promo.norm()).item()
+    assert rel < 2e-3, f"relative L2 to the promotion kernel {rel}"
+
+
+def test_fp8_gemm_nt_ue8m0_is_deterministic():
+    xq, xs, xs_dev, wq, ws = _ue8m0_inputs(35, 4099, 6144, 1280)
+    args = (xq.to(DEV), xs_dev, wq.to(DEV), ws.to(DEV))
+    first = K.fp8_gemm_nt(*args, ue8m0_scales=True)
+    for _ in range(3):
+        again = K.fp8_gemm_nt(*args, ue8m0_scales=True)
+        assert torch.equal(first.view(torch.int16), again.view(torch.int16))
+
+
+@pytest.mark.parametrize("M,I,Kd", [(1, 128, 128), (517, 9728, 256), (2048, 9728, 512)])
+def test_fp8_gemm_silu_quant_ue8m0_matches_pair(M, I, Kd):
+    """The UE8M0 gate_up kernel equals its own bf16 GEMM (qh_fp8_gemm_nt_ue8m0)
+    followed by silu_mul_quant(ue8m0) bit for bit."""
+    xq, xs, xs_dev, wq, ws = _ue8m0_inputs(40 + M, M, 2 * I, Kd)
+    args = (xq.to(DEV), xs_dev, wq.to(DEV), ws.to(DEV))
+    gate_up = K.fp8_gemm_nt(*args, ue8m0_scales=True)
+    q_pair, s_pair = K.silu_mul_quant(gate_up, True)
+    q, s = K.fp8_gemm_silu_quant(*args, ue8m0=True, ue8m0_scales=True)
+    assert torch.equal(s.cpu(), s_pair.cpu())
+    assert torch.equal(q.view(torch.uint8).cpu(), q_pair.view(torch.uint8).cpu())
+
+
 def test_fp8_gemm_silu_quant_oracle():
     """Against the oracle: fp64 GEMM rounded to bf16, then oracle silu_mul_quant."""
     g = _gen(13)
