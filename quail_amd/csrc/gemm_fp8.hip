@@ -267,7 +267,10 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
   // stages part of its output at a time in its own LDS slice (rows padded
   // so that the writes are bank-conflict free) and stores whole 128-byte row
   // segments, 16 bytes per lane. The slice is the wave's activation region, free
-  // between the read of its fragments and the next activation DMA.
+  // between the read of its fragments and the next activation DMA. The output
+  // is stored non-temporal: no later step of this kernel reads it, and left
+  // in L2 it would evict the activation and weight blocks the concurrent
+  // tiles share (1-4 % faster at 65k tokens).
   uint8_t* const slice = areg;
   auto store_bf16 = [&](const Cursor& c) __attribute__((always_inline)) {
     // eight passes, one per token half j and column quarter qd (n-tiles
@@ -297,8 +300,10 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
         const uint4 v = *reinterpret_cast<const uint4*>(slice + R * ROWB + chunk * 16);
         const int m = c.tm * BM + 32 * wave + 16 * j + R;
         if (m < M)
-          *reinterpret_cast<uint4*>(C + (long)m * ldc_b + (long)c.tn * BR * 2 + qd * 128 +
-                                    chunk * 16) = v;
+          __builtin_nontemporal_store(
+              __builtin_bit_cast(i32x4, v),
+              reinterpret_cast<i32x4*>(C + (long)m * ldc_b + (long)c.tn * BR * 2 + qd * 128 +
+                                       chunk * 16));
       }
     }
 #pragma unroll
@@ -344,7 +349,9 @@ __global__ __launch_bounds__(512, 1) void fp8_gemm_kernel(GemmArgs p) {
         const int R = 8 * q + (lane >> 3), chunk = lane & 7;
         const uint4 v = *reinterpret_cast<const uint4*>(slice + R * ROWB + chunk * 16);
         if (m_row + R < M)
-          *reinterpret_cast<uint4*>(out + (long)(m_row + R) * p.ldc + 128 * c.tn + chunk * 16) = v;
+          __builtin_nontemporal_store(
+              __builtin_bit_cast(i32x4, v),
+              reinterpret_cast<i32x4*>(out + (long)(m_row + R) * p.ldc + 128 * c.tn + chunk * 16));
       }
     }
   };
