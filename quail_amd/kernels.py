@@ -118,6 +118,8 @@ def fp8_gemm_silu_quant(a, a_scales, w, w_scales, ue8m0=False, ue8m0_scales=Fals
     M, N, K = _check_gemm(a, a_scales, w, w_scales)
     if N % (2 * GROUP):
         raise ValueError(f"gate_up rows {N} must be a multiple of 256")
+    if ue8m0_scales and not ue8m0:
+        raise ValueError("ue8m0_scales=True writes UE8M0 output scales: pass ue8m0=True")
     inter = N // 2
     q = torch.empty((M, inter), dtype=torch.float8_e4m3fn, device=a.device)
     scales = col_major_scales(M, inter, a.device)

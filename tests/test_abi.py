@@ -42,6 +42,12 @@ def test_argument_errors_raise_value_error_without_a_gpu():
     with pytest.raises(ValueError, match="multiple of 256"):
         _hip.call("qh_fp8_gemm_nt", None, 128, None, None, 128, None, None, 100,
                   4, 100, 128, None)
+    with pytest.raises(ValueError, match="fp8_gemm_nt_ue8m0: N=100 must be a multiple of 256"):
+        _hip.call("qh_fp8_gemm_nt_ue8m0", None, 128, None, None, 128, None, None, 100,
+                  4, 100, 128, None)
+    with pytest.raises(ValueError, match="fp8_gemm_silu_quant_ue8m0: I=100"):
+        _hip.call("qh_fp8_gemm_silu_quant_ue8m0", None, 128, None, None, 128, None, 4, 100,
+                  128, None, 100, None, None)
     with pytest.raises(ValueError, match="head_dim"):
         _hip.call("qh_attention", None, 0, 0, None, None, None, 0, None, 0, 16,
                   None, None, 0, None, None, None, 1, 1, 1, 32, 8, 64, 0.1, 1,
