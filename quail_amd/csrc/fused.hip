@@ -227,8 +227,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 // One launch, two kinds of workgroup. The first 3 T work as
 // qk_norm_rope_kernel (row t, 16 head slots each, the same per-head
 // arithmetic), writing q to q_out and k into its K page row. The last
-// ceil(T / 16) each take 16 rows' v from qkv, stage them in LDS and write V^T
-// with the row index fastest, as kv_scatter_kernel does.
+// ceil(T / 16) * n_kv each take one KV head's v of 16 rows from qkv, stage it
+// in LDS and write V^T with the row index fastest, as kv_scatter_kernel does.
 constexpr int kRopeRows = 16;
 
 __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
     float eps, int T, int n_q, int n_kv, int slot_blocks, uint16_t* __restrict__ q_out,
     uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
     const int64_t* __restrict__ dst, int page) {
-  extern __shared__ uint16_t vbuf[];  // [row][n_kv * 128 + 2]
+  extern __shared__ uint16_t vbuf[];  // [row][128 + 2] of one KV head
   const long head_blocks = (long)T * slot_blocks;
   const int j = threadIdx.x & 15;
   if ((long)blockIdx.x < head_blocks) {
@@ -258,30 +258,30 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kv_kernel(
     }
     return;
   }
-  const int row_elems = n_kv * 128;
-  const int ld = row_elems + 2;
-  const int t0 = (int)(blockIdx.x - head_blocks) * kRopeRows;
+  // V^T workgroups: 16 rows of one KV head each, so the LDS staging is 4 KiB
+  // and does not limit how many head workgroups share a CU
+  const long vb = (long)blockIdx.x - head_blocks;
+  const int h = (int)(vb % n_kv);
+  const int t0 = (int)(vb / n_kv) * kRopeRows;
   const int rows = min(kRopeRows, T - t0);
-  const int chunks = rows * n_kv * 16;  // 16-byte chunks of the rows' v
-  const uint16_t* vsrc = qkv + (long)(n_q + n_kv) * 128;
-  for (int c = threadIdx.x; c < chunks; c += 256) {
-    const int e = c / (n_kv * 16), hc = c % (n_kv * 16);
+  constexpr int ld = 128 + 2;
+  const uint16_t* vsrc = qkv + (long)(n_q + n_kv + h) * 128;
+  for (int c = threadIdx.x; c < rows * 16; c += 256) {
+    const int e = c >> 4, hc = c & 15;
     const bf16x8 vv = load8(vsrc + (long)(t0 + e) * ld_qkv + hc * 8);
     uint32_t* vl = reinterpret_cast<uint32_t*>(vbuf + e * ld + hc * 8);
 #pragma unroll
     for (int w = 0; w < 4; ++w) vl[w] = vv.w[w];
   }
   __syncthreads();
-  // V^T: work item = (head, d, row), row fastest
-  const int items = row_elems * kRopeRows;
-  for (int it = threadIdx.x; it < items; it += 256) {
+  // V^T: work item = (d, row), row fastest
+  for (int it = threadIdx.x; it < 128 * kRopeRows; it += 256) {
     const int e = it & (kRopeRows - 1);
     if (e >= rows) continue;
-    const int hd = it >> 4;  // h * 128 + d
+    const int d = it >> 4;
     const long r = dst[t0 + e];
     const long pg = r / page, sl = r % page;
-    const int h = hd >> 7, d = hd & 127;
-    v_pool[((pg * n_kv + h) * 128 + d) * page + sl] = vbuf[e * ld + hd];
+    v_pool[((pg * n_kv + h) * 128 + d) * page + sl] = vbuf[e * ld + d];
   }
 }
 
@@ -576,15 +576,14 @@ extern "C" int qh_qk_norm_rope_kv(const void* qkv, long ld_qkv, const int64_t* p
   QH_REQUIRE(d == 128, "qk_norm_rope_kv: head_dim %d unsupported (128 only)", d);
   QH_REQUIRE(n_q > 0 && n_kv > 0 && T >= 0 && max_pos > 0 && page_tokens > 0,
              "qk_norm_rope_kv: geometry");
-  QH_REQUIRE(n_kv <= 15, "qk_norm_rope_kv: n_kv=%d exceeds the 64 KiB staging buffer", n_kv);
   QH_REQUIRE(ld_qkv >= (long)(n_q + 2 * n_kv) * d && ld_qkv % 8 == 0,
              "qk_norm_rope_kv: row stride %ld", ld_qkv);
   if (T == 0) return QH_OK;
   QH_REQUIRE(qkv && positions && cos_sin && qw && kw && q_out && k_pool && v_pool && dst,
              "qk_norm_rope_kv: null pointer");
-  const size_t smem = (size_t)kRopeRows * (n_kv * 128 + 2) * sizeof(uint16_t);
+  const size_t smem = (size_t)kRopeRows * (128 + 2) * sizeof(uint16_t);
   const int slot_blocks = blocks_for(n_q + n_kv, 16);
-  const long grid = (long)T * slot_blocks + blocks_for(T, kRopeRows);
+  const long grid = (long)T * slot_blocks + (long)blocks_for(T, kRopeRows) * n_kv;
   QH_REQUIRE(grid < 0x7fffffffL, "qk_norm_rope_kv: %d rows exceed the grid", T);
   hipLaunchKernelGGL(qk_norm_rope_kv_kernel, dim3((unsigned)grid), dim3(256), smem,
                      (hipStream_t)stream, (const uint16_t*)qkv, ld_qkv, positions,

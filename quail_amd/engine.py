@@ -44,7 +44,7 @@ class Engine:
 
     def __init__(self, arena, *, n_q, n_kv, head_dim, rotary, fp8=True,
                  kernels_name="quail", ue8m0=False, gemm_hook=None,
-                 attention_hook=None, tree_kernel="fused", fuse_kv_write=False):
+                 attention_hook=None, tree_kernel="fused", fuse_kv_write=True):
         import torch
         if tree_kernel not in ("fused", "two_pass"):
             raise ValueError(f"tree_kernel must be 'fused' or 'two_pass', got {tree_kernel!r}")

@@ -33,7 +33,7 @@ class Qwen3Pipeline(ModelPipeline):
 
     def __init__(self, model, arena, *, spec=None, kernels_name="quail",
                  engine_class=Engine, ue8m0=False, gemm_hook=None, attention_hook=None,
-                 tree_kernel="fused", fuse_kv_write=False):
+                 tree_kernel="fused", fuse_kv_write=True):
         import torch
         self.layers = model.model.layers
         self.embed = model.model.embed_tokens
