@@ -780,19 +780,33 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
   // swizzle kswz(16 pit + r16) = r16 ^ pit; own V's vswz = 4 (r16 % 4) =
   // 4 (lane / 16); a node V^T row d = 32c + lane/2 swaps its halves when
   // (d / 8) is odd, i.e. when (lane / 16) is odd. Computed per piece from
-  // the lane, to keep registers for the tile loop.
-  const int l16 = lane >> 4, pc = lane & 15;
-  const uint32_t k_chunk = (uint32_t)((pc ^ l16 ^ pit) * 16);  // XOR 64 c per piece
-  const uint32_t own_v_chunk = (uint32_t)((pc ^ (4 * l16)) * 16);
-  const uint32_t node_v_off = (uint32_t)((lane >> 1) * 32 + (((lane & 1) ^ (l16 & 1)) * 16));
-  const uint32_t own_row = (uint32_t)l16 * row_bytes + (uint32_t)hk * 256u;
-  auto voff_node = [&](int c) __attribute__((always_inline)) {
-    return region == 0 ? (uint32_t)((4 * c + l16) * 256) + (k_chunk ^ (uint32_t)(64 * c))
-                       : node_v_off + (uint32_t)(1024 * c);
+  // the lane, to keep registers for the tile loop: the lane id is re-read
+  // (v_mbcnt, opaque to the compiler) at every DMA, so none of these offsets
+  // is held across the loop - held, they were spilled, and the reload's
+  // vmcnt(0) wait drained the DMA ring before every tile.
+  struct LaneOff {
+    uint32_t k_chunk, own_v_chunk, node_v_off, own_row;
+    int l16;
   };
-  auto voff_own = [&](int c) __attribute__((always_inline)) {
-    return own_row + (uint32_t)(4 * c) * row_bytes +
-           (region == 0 ? (k_chunk ^ (uint32_t)(64 * c)) : own_v_chunk);
+  auto lane_offsets = [&]() __attribute__((always_inline)) {
+    int ln;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    LaneOff o;
+    o.l16 = ln >> 4;
+    const int pc = ln & 15;
+    o.k_chunk = (uint32_t)((pc ^ o.l16 ^ pit) * 16);  // XOR 64 c per piece
+    o.own_v_chunk = (uint32_t)((pc ^ (4 * o.l16)) * 16);
+    o.node_v_off = (uint32_t)((ln >> 1) * 32 + (((ln & 1) ^ (o.l16 & 1)) * 16));
+    o.own_row = (uint32_t)o.l16 * row_bytes + (uint32_t)hk * 256u;
+    return o;
+  };
+  auto voff_node = [&](const LaneOff& o, int c) __attribute__((always_inline)) {
+    return region == 0 ? (uint32_t)((4 * c + o.l16) * 256) + (o.k_chunk ^ (uint32_t)(64 * c))
+                       : o.node_v_off + (uint32_t)(1024 * c);
+  };
+  auto voff_own = [&](const LaneOff& o, int c) __attribute__((always_inline)) {
+    return o.own_row + (uint32_t)(4 * c) * row_bytes +
+           (region == 0 ? (o.k_chunk ^ (uint32_t)(64 * c)) : o.own_v_chunk);
   };
   const uint16_t* pool = region ? p.v_pool : p.k_pool;
   const uint16_t* own_rows = region ? p.v_rows : p.k_rows;
@@ -811,6 +825,7 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
     const uint32_t base =
         (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(
             lds + (t % NST) * STAGE + region * HALF + pit * 4096);
+    const LaneOff lo = lane_offsets();
     if (t < n1) {
       const int pidx = 2 * t + pit;
       const bool live = pidx < p.table_width && pidx * PAGE < node_keys && page_id >= 0 &&
@@ -825,7 +840,7 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
             "s_mov_b32 m0, %0\n\t"
             "buffer_load_dwordx4 %1, %2, 0 offen lds"
             :
-            : "s"(base + 1024 * c), "v"(voff_node(c)), "s"(rs)
+            : "s"(base + 1024 * c), "v"(voff_node(lo, c)), "s"(rs)
             : "memory", "m0");
     } else {
       // own keys 32 (t - n1) + 16 pit + 0..15: chunk rows q0 + those keys;
@@ -841,7 +856,7 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
             "s_mov_b32 m0, %0\n\t"
             "buffer_load_dwordx4 %1, %2, 0 offen lds"
             :
-            : "s"(base + 1024 * c), "v"(voff_own(c)), "s"(rs)
+            : "s"(base + 1024 * c), "v"(voff_own(lo, c)), "s"(rs)
             : "memory", "m0");
     }
   };
