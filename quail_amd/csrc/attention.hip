@@ -333,10 +333,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
 // one wave per head) but with 32-key tiles that reach LDS by DMA
 // (buffer_load ... lds) straight from the arena's 4 KiB page blocks, in a
 // 3-stage ring two tiles ahead, and with about half the registers, so three
-// workgroups share a CU. Per tile each wave issues exactly five vector-memory
-// loads - the page id it needs for tile t+3, then its four 1 KiB DMA pieces
-// of tile t+2 (wave w moves K (w < 2) or V^T (w >= 2) of page w % 2) - so
-// every wait is vmcnt(4).
+// workgroups share a CU. Per tile each wave issues exactly four vector-memory
+// loads - its four 1 KiB DMA pieces of tile t+2 (wave w moves K (w < 2) or
+// V^T (w >= 2) of page w % 2) - and one scalar load, the page id it needs
+// for tile t+3, so every wait is vmcnt(4).
 //
 // LDS stage: K [32 keys][128 d] with 16-byte chunks XOR-swizzled by
 // (key % 16) ^ (key / 16); V^T [2 pages][128 d][16 slots] with the two
@@ -445,16 +445,11 @@ __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
     }
   }
   const uint16_t* pool = region ? p.v_pool : p.k_pool;
-  const pi32x4 rtab = attn_rsrc(p.table, (uint32_t)p.n_seqs * (uint32_t)p.table_width * 4u);
   const long tab_row = (long)s * p.table_width;
   // page index of this wave's page in tile t, clamped into the table row
   auto tab_off = [&](int t) __attribute__((always_inline)) {
     const int pidx = min(2 * t + pit, p.table_width - 1);
     return (uint32_t)((tab_row + pidx) * 4);
-  };
-  auto load_page_id = [&](int t, float& dst) __attribute__((always_inline)) {
-    asm volatile("buffer_load_dword %0, off, %1, %2"
-                 : "=v"(dst) : "s"(rtab), "s"(tab_off(t)) : "memory");
   };
   // this wave's four DMA pieces of tile t into stage t % NST
   auto dma_tile = [&](int t, int page_id) __attribute__((always_inline)) {
@@ -518,21 +513,19 @@ __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
     for (int a = 0; a < 16; ++a) acc_o[db][a] = 0.f;
   float m_run = -1e30f;   // finite floor: see the softmax note in the tile loop
   float l_run = 0.f;
-  float pg_next = __builtin_bit_cast(float, pg2);  // page id for the DMA of tile t+2
+  int pg_next = pg2;  // page id for the DMA of tile t+2
 
   const int kq = kperm(col);  // key row this lane's S^T row reads
   for (int t = 0; t < n_tiles; ++t) {
     // tile t's DMA (issued two tiles back) and the page id of tile t+2
     // (issued first last tile) have landed; tile t+1's DMA may be in flight
     asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    asm volatile("" : "+v"(pg_next));
-    const int page_t2 = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, pg_next));
+    const int page_t2 = pg_next;
     // stage t visible to all (every wave waited for its share above); stage
     // t-1 free. A plain barrier: __syncthreads' fence would also wait for
     // the DMA of tile t+1.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    load_page_id(t + 3, pg_next);
     dma_tile(t + 2, page_t2);
 
     uint8_t* st_base = lds + (t % NST) * STAGE;
@@ -621,6 +614,13 @@ __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
         acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, acc_o[db], 0, 0, 0);
       }
     }
+    // the page id of tile t+3 by a scalar load (the table is read-only for
+    // the kernel: constant address space), issued last so that its latency
+    // hides behind the next tile's DMA wait. A vector load, whose result the
+    // compiler would wait for with vmcnt(0) - it cannot see the DMA loads -
+    // drained the DMA ring at every tile.
+    pg_next = ((const __attribute__((address_space(4))) int32_t*)(uintptr_t)(p.table))[
+        tab_off(t + 3) / 4];
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outlives the workgroup
 
@@ -810,15 +810,10 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
   };
   const uint16_t* pool = region ? p.v_pool : p.k_pool;
   const uint16_t* own_rows = region ? p.v_rows : p.k_rows;
-  const pi32x4 rtab = attn_rsrc(p.table, r >= 0 ? (uint32_t)p.n_reads * (uint32_t)p.table_width * 4u : 0u);
   const long tab_row = (long)(r >= 0 ? r : 0) * p.table_width;
   auto tab_off = [&](int t) __attribute__((always_inline)) {
     const int pidx = min(2 * t + pit, p.table_width - 1);
     return (uint32_t)((tab_row + max(pidx, 0)) * 4);
-  };
-  auto load_page_id = [&](int t, float& dst) __attribute__((always_inline)) {
-    asm volatile("buffer_load_dword %0, off, %1, %2"
-                 : "=v"(dst) : "s"(rtab), "s"(tab_off(t)) : "memory");
   };
   // this wave's four DMA pieces of tile t into stage t % NST
   auto dma_tile = [&](int t, int page_id) __attribute__((always_inline)) {
@@ -897,7 +892,7 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
     for (int a = 0; a < 16; ++a) acc_o[db][a] = 0.f;
   float m_run = -1e30f;   // finite floor: see the softmax note in the tile loop
   float l_run = 0.f;
-  float pg_next = __builtin_bit_cast(float, pg2);
+  int pg_next = pg2;
 
   // own-tile P.V operand addresses (see the note above the kernel): lane
   // group G = lane / 16 covers d = 32 db + 16 (G % 2) + lane % 16 and keys
@@ -918,14 +913,12 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
   auto tile = [&](int t, auto node_c) __attribute__((always_inline)) {
     constexpr bool node = decltype(node_c)::value;
     asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    asm volatile("" : "+v"(pg_next));
-    const int page_t2 = __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, pg_next));
+    const int page_t2 = pg_next;
     // stage t visible to all (every wave waited for its share above); stage
     // t-1 free. A plain barrier: __syncthreads' fence would also wait for
     // the DMA of tile t+1.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    load_page_id(t + 3, pg_next);
     dma_tile(t + 2, page_t2);
 
     uint8_t* st_base = lds + (t % NST) * STAGE;
@@ -1044,6 +1037,11 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
         }
       }
     }
+    // the page id of node tile t+3 by a scalar load, last (as attn_paged_kernel)
+    pg_next = (r >= 0 && t + 3 < n1)
+                  ? ((const __attribute__((address_space(4))) int32_t*)(uintptr_t)(p.table))[
+                        tab_off(t + 3) / 4]
+                  : 0;
   };
   for (int t = 0; t < n1; ++t) tile(t, std::true_type{});
   for (int t = n1; t < n_tiles; ++t) tile(t, std::false_type{});
