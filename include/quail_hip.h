@@ -415,6 +415,26 @@ int qh_answer_bits(const void* normed, int R, int H, const void* w_ans,
                    int n_ans, const uint8_t* is_true, uint8_t* bits,
                    float* margin, qh_stream_t stream);
 
+/*
+ * The e4m3 encoder of the fused epilogues (attention, gate_up), which leave
+ * out the reference's +-448 clamp (attention.py:318) because their inputs
+ * never exceed 448 (1 + 2^-24) in magnitude: x [n] fp32 (16-byte aligned,
+ * n a multiple of 4) -> out [n] e4m3 bytes, scale 1. No reference
+ * counterpart: it exposes the encoder so its saturation of (448, 464] to
+ * +-448 is checked on the device.
+ */
+int qh_e4m3_encode(const float* x, long n, uint8_t* out, qh_stream_t stream);
+
+/*
+ * AnswerRows.logits (readout.py:45-49): per row, the largest bf16 score
+ * over the TRUE columns and over the FALSE columns, the same scores
+ * qh_answer_bits compares.
+ *   best_true, best_false [R] bf16 (device).
+ */
+int qh_answer_logits(const void* normed, int R, int H, const void* w_ans,
+                     int n_ans, const uint8_t* is_true, void* best_true,
+                     void* best_false, qh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -83,8 +83,9 @@ int qp_arena_grow(void* arena, int64_t key, int64_t capacity, int64_t* added);
 int qp_arena_pin(void* arena, int64_t key);
 /* Pages of the key's table no other key holds. */
 int64_t qp_arena_sole_pages(const void* arena, int64_t key);
-/* PageArena.retain (arena.py:153-179): priority tuple of n_priority (<= 2)
- * doubles, or the default (tokens per sole page) with n_priority 0. */
+/* PageArena.retain (arena.py:153-179): a priority tuple of n_priority
+ * doubles of any length, compared lexicographically as Python compares
+ * tuples, or the default (tokens per sole page) when priority is NULL. */
 int qp_arena_retain(void* arena, int64_t key, const double* priority, int32_t n_priority);
 /* PageArena.pop_retained_victim (arena.py:192-212): out[3] = key, pages,
  * tokens; QP_NONE when no retained key outside `keep` is left. */

@@ -199,30 +199,6 @@ def fp8_gemm(a_q, a_scales, w_q, w_scales, out_dtype=torch.bfloat16):
     return out.to(out_dtype)
 
 
-def fp8_gemm_blockwise_fp32(a_q, a_scales, w_q, w_scales, out_dtype=torch.bfloat16):
-    """The same sum accumulated as a per-block promotion in fp32.
-
-    Each 128-deep block product is exact (fp8 products summed in fp64),
-    rounded once to fp32; the block's combined scale s = fp32(sa * sb) is
-    applied with one fused multiply-add into an fp32 accumulator, blocks in
-    K order: acc = fp32(acc + fp32(block) * s). This is DeepGEMM's promotion
-    scheme (per-128-K fp32 promotion) written out, and the order the gfx950
-    kernel accumulates in.
-    """
-    M, K = a_q.shape
-    N = w_q.shape[0]
-    kb_n = K // GROUP
-    a = a_q.double().view(M, kb_n, GROUP)
-    w = w_q.double().view(N, kb_n, GROUP)
-    sb = w_scales.float().repeat_interleave(GROUP, dim=0)   # [N, kb]
-    acc = torch.zeros(M, N, dtype=torch.float32, device=a_q.device)
-    for kb in range(kb_n):
-        block = (a[:, kb, :] @ w[:, kb, :].T).float()
-        s = a_scales[:, kb].float()[:, None] * sb[:, kb][None, :]
-        acc = (acc.double() + block.double() * s.double()).float()
-    return acc.to(out_dtype)
-
-
 # ---------------------------------------------------------------- attention
 
 def attend(q, k, v, scale, visible):

@@ -72,6 +72,8 @@ SIGNATURES = {
     "qh_final_norm": [_p, _p, _p, _i, _i, _p, _f, _p, _p],
     "qh_fused_add_rms_norm": [_p, _p, _i, _i, _p, _f, _p],
     "qh_answer_bits": [_p, _i, _i, _p, _i, _p, _p, _p, _p],
+    "qh_answer_logits": [_p, _i, _i, _p, _i, _p, _p, _p, _p],
+    "qh_e4m3_encode": [_p, _l, _p, _p],
 }
 
 RESTYPES = {

@@ -70,21 +70,35 @@ class TemporaryKey:
 
 
 class _Keys:
-    """Caller keys <-> library handles (positive; temporaries are negative)."""
+    """Caller keys <-> library handles (positive; temporaries are negative).
+
+    Handles are numbered from 1 and never reused, so a handle the library
+    still mentions can never name another key; a key's entry is dropped by
+    forget() once the library holds nothing under it."""
 
     def __init__(self):
         self._handles = {}
         self._keys = {}
+        self._next = 1
 
     def handle(self, key):
         if isinstance(key, TemporaryKey):
             return key.handle
         h = self._handles.get(key)
         if h is None:
-            h = len(self._handles) + 1
+            h = self._next
+            self._next += 1
             self._handles[key] = h
             self._keys[h] = key
         return h
+
+    def forget(self, key):
+        h = self._handles.pop(key, None)
+        if h is not None:
+            del self._keys[h]
+
+    def __len__(self):
+        return len(self._handles)
 
     def known(self, key):
         """The handle of a key seen before, else None."""
@@ -240,6 +254,14 @@ class PageArena:
     def pin(self, key) -> None:
         self._call("qp_arena_pin", self._require(key))
 
+    def forget(self, keys) -> None:
+        """Drop the handles of `keys` that are no longer resident (freed or
+        evicted): a finished stream calls this for its keys, so a long
+        session's handle table holds only what the arena still holds."""
+        for key in keys:
+            if not isinstance(key, TemporaryKey) and not self._resident(key):
+                self._keys.forget(key)
+
     def retain(self, key, priority=None) -> None:
         """Make a resident key evictable after its current use (arena.py:153-179).
         Priority: the given tuple, the policy's, or tokens per page the key
@@ -253,8 +275,9 @@ class PageArena:
             self._call("qp_arena_retain", h, None, 0)
             return
         values = tuple(priority) if isinstance(priority, (tuple, list)) else (priority,)
-        p = np.asarray(values, dtype=np.float64)
-        self._call("qp_arena_retain", h, p.ctypes.data, int(p.size))
+        p = np.zeros(max(1, len(values)), dtype=np.float64)
+        p[:len(values)] = values
+        self._call("qp_arena_retain", h, p.ctypes.data, len(values))
 
     def configure_retention(self, policy, cap_pages: int) -> None:
         if not 0 <= cap_pages <= self.n_pages:
@@ -553,6 +576,10 @@ class KVArena:
         """Free a key's pages now, or once its last hold is released."""
         return self._call("qp_arena_free_key", self.accounting._require(key))
 
+    def forget(self, keys) -> None:
+        """Drop the key handles of `keys` the arena no longer holds."""
+        self.accounting.forget(keys)
+
     # ---- residency --------------------------------------------------------
 
     @property
@@ -634,13 +661,13 @@ class KVArena:
         return self.k[layer], self.v[layer]
 
     def layer_kv(self, layer: int):
-        """The reference's flat (rows, n_kv, d) pools (arena.py:851-855) do not
-        exist in this arena; a view of them cannot be built without a copy,
-        so this raises instead of handing out the physical layout."""
-        raise NotImplementedError(
-            "this arena stores K as [pages, n_kv, 16, d] and V as [pages, n_kv, d, 16]; "
-            "use page_pools() for the kernels' layout or paged_kv() for the "
-            "(pages, 16, n_kv, d) views")
+        """K and V of one layer addressed by the reference's flat arena rows
+        (arena.py:851-855): row page * 16 + slot holds [n_kv, d]. No flat
+        view of the MI355X pools exists, so these are row-indexed pools
+        (layout.RowPool): indexing reads rows, assignment writes them into
+        the pages. The kernels take page_pools()."""
+        k, v = self.paged_kv(layer)
+        return layout.RowPool(k), layout.RowPool(v)
 
     def paged_kv(self, layer: int):
         """K and V as the reference's (n_pages, 16, n_kv, d) paged views

@@ -498,7 +498,8 @@ __global__ __launch_bounds__(256) void answer_bits_kernel(
     const uint16_t* __restrict__ normed, int R, int H,
     const uint16_t* __restrict__ w_ans, int n_ans,
     const uint8_t* __restrict__ is_true, uint8_t* __restrict__ bits,
-    float* __restrict__ margin) {
+    float* __restrict__ margin, uint16_t* __restrict__ best_true,
+    uint16_t* __restrict__ best_false) {
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= R) return;
   const int lane = threadIdx.x & 63;
@@ -517,9 +518,22 @@ __global__ __launch_bounds__(256) void answer_bits_kernel(
     else best_f = fmaxf(best_f, score);
   }
   if (lane == 0) {
-    bits[i] = best_t > best_f ? 1 : 0;
+    if (bits) bits[i] = best_t > best_f ? 1 : 0;
     if (margin) margin[i] = best_t - best_f;
+    // the scores are bf16 values already: the top 16 bits are exact
+    if (best_true) best_true[i] = (uint16_t)(__float_as_uint(best_t) >> 16);
+    if (best_false) best_false[i] = (uint16_t)(__float_as_uint(best_f) >> 16);
   }
+}
+
+// The fused epilogues' e4m3 encoder (quant_e4m3_x4, no +-448 clamp) over
+// raw fp32 values with scale 1: four values per thread.
+__global__ __launch_bounds__(256) void e4m3_encode_kernel(const float* __restrict__ x,
+                                                          long n4, uint32_t* __restrict__ out) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const float4 v = reinterpret_cast<const float4*>(x)[i];
+  out[i] = quant_e4m3_x4(v.x, v.y, v.z, v.w, 1.0);
 }
 
 }  // namespace qh
@@ -738,6 +752,31 @@ extern "C" int qh_answer_bits(const void* normed, int R, int H, const void* w_an
   QH_REQUIRE(normed && w_ans && is_true && bits, "answer_bits: null pointer");
   hipLaunchKernelGGL(answer_bits_kernel, dim3(blocks_for(R, 4)), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)normed, R, H,
-                     (const uint16_t*)w_ans, n_ans, is_true, bits, margin);
+                     (const uint16_t*)w_ans, n_ans, is_true, bits, margin,
+                     (uint16_t*)nullptr, (uint16_t*)nullptr);
   return launch_status("answer_bits");
+}
+
+extern "C" int qh_e4m3_encode(const float* x, long n, uint8_t* out, qh_stream_t stream) {
+  QH_REQUIRE(n >= 0 && n % 4 == 0, "e4m3_encode: n=%ld must be a multiple of 4", n);
+  if (n == 0) return QH_OK;
+  QH_REQUIRE(x && out, "e4m3_encode: null pointer");
+  QH_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 3) == 0, "e4m3_encode: alignment");
+  hipLaunchKernelGGL(e4m3_encode_kernel, dim3(blocks_for(n / 4, 256)), dim3(256), 0,
+                     (hipStream_t)stream, x, n / 4, (uint32_t*)out);
+  return launch_status("e4m3_encode");
+}
+
+extern "C" int qh_answer_logits(const void* normed, int R, int H, const void* w_ans,
+                                int n_ans, const uint8_t* is_true, void* best_true,
+                                void* best_false, qh_stream_t stream) {
+  QH_REQUIRE(R >= 0 && H > 0 && H % 8 == 0 && n_ans > 0, "answer_logits: geometry");
+  if (R == 0) return QH_OK;
+  QH_REQUIRE(normed && w_ans && is_true && best_true && best_false,
+             "answer_logits: null pointer");
+  hipLaunchKernelGGL(answer_bits_kernel, dim3(blocks_for(R, 4)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)normed, R, H,
+                     (const uint16_t*)w_ans, n_ans, is_true, (uint8_t*)nullptr,
+                     (float*)nullptr, (uint16_t*)best_true, (uint16_t*)best_false);
+  return launch_status("answer_logits");
 }

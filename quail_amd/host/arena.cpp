@@ -34,11 +34,13 @@ namespace {
 // Heap order: smaller priority first (lexicographic, a shorter tuple before
 // a longer one it prefixes), then older retain first.
 bool entry_after(const RetainEntry& a, const RetainEntry& b) {
-  const int n = std::min(a.priority.n, b.priority.n);
-  for (int i = 0; i < n; ++i) {
-    if (a.priority.v[i] != b.priority.v[i]) return a.priority.v[i] > b.priority.v[i];
+  const std::vector<double>& x = a.priority.v;
+  const std::vector<double>& y = b.priority.v;
+  const size_t n = std::min(x.size(), y.size());
+  for (size_t i = 0; i < n; ++i) {
+    if (x[i] != y[i]) return x[i] > y[i];
   }
-  if (a.priority.n != b.priority.n) return a.priority.n > b.priority.n;
+  if (x.size() != y.size()) return x.size() > y.size();
   return a.version > b.version;
 }
 
@@ -191,8 +193,7 @@ void Arena::retain(int64_t key, const Priority* priority) {
   if (priority) {
     e.priority = *priority;
   } else {
-    e.priority.n = 1;
-    e.priority.v[0] = (double)s.tokens / (double)std::max<int64_t>(1, pages);
+    e.priority.v.assign(1, (double)s.tokens / (double)std::max<int64_t>(1, pages));
   }
   e.version = s.retained_version;
   e.key = key;

@@ -184,11 +184,10 @@ int64_t qp_arena_sole_pages(const void* arena, int64_t key) {
 
 int qp_arena_retain(void* arena, int64_t key, const double* priority, int32_t n_priority) {
   return (int)guarded([&] {
-    if (n_priority < 0 || n_priority > 2) fail(kValueError, "priority tuples hold at most 2 values");
+    if (n_priority < 0) fail(kValueError, "priority of %d values", (int)n_priority);
     Priority p;
-    p.n = n_priority;
-    for (int i = 0; i < n_priority; ++i) p.v[i] = priority[i];
-    as<Arena>(arena, "arena")->retain(key, n_priority ? &p : nullptr);
+    if (priority) p.v.assign(priority, priority + n_priority);
+    as<Arena>(arena, "arena")->retain(key, priority ? &p : nullptr);
     return (int64_t)kOk;
   });
 }

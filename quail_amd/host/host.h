@@ -33,9 +33,12 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Page arena: page accounting plus the borrower holds, deferred frees and
 // retention of the KV arena. Keys are integer handles chosen by the caller
 // (temporaries get negative handles from the arena itself).
+// A retention priority: a tuple of numbers compared lexicographically, as
+// Python compares the tuples a retention policy returns (arena.py:170-179;
+// cost/retention.py:19-25 returns three: value per page, -next use,
+// -document).
 struct Priority {
-  double v[2] = {0.0, 0.0};
-  int n = 1;
+  std::vector<double> v;
 };
 
 struct KeyState {

@@ -442,3 +442,23 @@ def answer_bits(normed, w_ans, is_true, with_margin=True):
     _hip.call("qh_answer_bits", _ptr(normed), R, H, _ptr(w_ans), w_ans.shape[0],
               _ptr(is_true), _ptr(bits), _ptr(margin), _stream())
     return bits, margin
+
+
+def e4m3_encode(x):
+    """fp32 values -> e4m3 through the fused epilogues' encoder (no clamp)."""
+    _check(x, torch.float32, "x", dim=1)
+    n = x.shape[0]
+    out = torch.empty(n, dtype=torch.uint8, device=x.device)
+    _hip.call("qh_e4m3_encode", _ptr(x), n, _ptr(out), _stream())
+    return out
+
+
+def answer_logits(normed, w_ans, is_true):
+    """Per row, the best bf16 score of each class (readout.py:45-49)."""
+    _check(normed, torch.bfloat16, "normed", dim=2)
+    R, H = normed.shape
+    best_t = torch.empty(R, dtype=torch.bfloat16, device=normed.device)
+    best_f = torch.empty(R, dtype=torch.bfloat16, device=normed.device)
+    _hip.call("qh_answer_logits", _ptr(normed), R, H, _ptr(w_ans), w_ans.shape[0],
+              _ptr(is_true), _ptr(best_t), _ptr(best_f), _stream())
+    return best_t, best_f

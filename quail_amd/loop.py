@@ -499,6 +499,7 @@ class FilterStream:
         for doc in self.sched.drain_ready():
             self.arena.free_key(self.keys[doc])
         self.arena.drop_holds(self._parents)
+        self.arena.forget(self.keys)
         self.done = True
 
     def _admit(self, items, evict_retained):
@@ -826,6 +827,7 @@ class _Join:
         while self.outstanding:
             self.report(self.outstanding.pop(0))
         arena.drop_holds(self.held)
+        arena.forget(self.keys)
 
 
 def run_join(torch, arena, pipeline, async_ans, anchor_prefixes, stage_suffixes, budget,

@@ -22,6 +22,11 @@ class AnswerRows:
         mask = [1 if t in true_ids else 0 for t in self.allowed]
         self.is_true = torch.tensor(mask, dtype=torch.uint8, device=self.weights.device)
 
+    def logits(self, normed):
+        """Per row, the best logit of each class over its spellings: bf16
+        (best TRUE, best FALSE), as readout.py:45-49 returns them."""
+        return kernels.answer_logits(normed, self.weights, self.is_true)
+
     def bits(self, normed, with_margin=False):
         return kernels.answer_bits(normed, self.weights, self.is_true, with_margin)
 

@@ -32,10 +32,42 @@ def _runs(rows):
     return out
 
 
+def _key(k):
+    """JSON keys: a string, or an [alias, document] pair (a tuple key)."""
+    return tuple(k) if isinstance(k, list) else k
+
+
+def _plain(v):
+    """Tuple keys back to lists, to compare with JSON."""
+    if isinstance(v, (tuple, list)):
+        return [_plain(x) for x in v]
+    return v
+
+
+class _Policy:
+    """A retention policy of the reference's shape (cost/retention.py:19-25)
+    with seconds = tokens: (probability * tokens / pages, -next_use,
+    -document), uses = {alias: (probability, next_use)}."""
+
+    def __init__(self, uses):
+        self.uses = uses
+
+    def priority(self, key, tokens, pages):
+        alias, document = key
+        probability, next_use = self.uses.get(alias, (0.0, 0))
+        return (probability * tokens / pages, -next_use, -document)
+
+
 def _apply(a, op, args):
+    args = [_key(args[0])] + list(args[1:]) if args and op != "configure" else args
+    if op == "configure":
+        uses, cap = args
+        return a.configure_retention(_Policy({k: tuple(v) for k, v in uses.items()}), cap)
+    if op == "retain" and len(args) == 2:
+        return a.retain(args[0], tuple(args[1]))
     if op == "alloc":
         key, tokens, capacity, borrow = args
-        borrowed = a.shared_pages(*borrow) if borrow else ()
+        borrowed = a.shared_pages(_key(borrow[0]), *borrow[1:]) if borrow else ()
         return a.alloc(key, tokens, capacity, borrowed=borrowed)
     if op == "shared_pages":
         return a.shared_pages(*args)
@@ -51,7 +83,7 @@ def _apply(a, op, args):
         return _runs(a.row_indices(*args))
     if op == "pop_victim":
         v = a.pop_retained_victim()
-        return None if v is None else list(v)
+        return None if v is None else _plain(v)
     raise AssertionError(f"unknown op {op}")
 
 
@@ -71,7 +103,7 @@ def test_known_answers(case):
         if op == "state":
             assert _state(a, entry[1]) == entry[1], f"{case['name']} step {step}"
             continue
-        if op in ("pin", "retain"):
+        if op in ("pin", "retain", "configure"):
             _apply(a, op, entry[1:])
             continue
         args, want = entry[1:-1], entry[-1]
@@ -180,3 +212,36 @@ def test_held_keys_are_never_evicted_and_drop_holds_frees_in_hold_order():
     assert arena.is_resident(("a", 1))
     assert arena.drop_holds() and not arena.is_resident(("a", 1))
     assert not arena.drop_holds()
+
+
+
+def test_finished_streams_leave_no_handles_behind():
+    """A long session runs many filters over one arena: once a stream ends,
+    the handle table holds only the keys the arena still holds (here the
+    survivors retained for a later operator), and no handle number is
+    handed out twice."""
+    import torch
+
+    from kv_checker import HashModel, _Passthrough, _Pipeline, answer, chain
+    from quail_amd import loop
+
+    arena = KVArena(n_layers=1, n_pages=256, page_tokens=16, n_kv=1, d_head=1,
+                    dtype=torch.float32, device="cpu", allocate=False)
+    seen = set()
+    for round_ in range(3):
+        docs = [[7 + round_, 100 + d, 200 + d] * (1 + d % 3) for d in range(20)]
+        question = [5, 6]
+        answers = {}
+        for doc in docs:
+            hv = chain(list(doc) + question)
+            answers[hv] = answer(hv)
+        keys = [("q%d" % round_, d) for d in range(20)]
+        got, _, _ = loop.run_filter(torch, arena, _Pipeline(HashModel(arena, answers)),
+                                    _Passthrough(), docs, [question], 64, arena_writes=True,
+                                    arena_keys=keys, retain_survivors={0, 1, 2, 3})
+        kept = {keys[d] for d in range(4) if got[d][-1]}
+        assert kept <= set(arena.resident_keys())
+        handles = {arena.handle(k) for k in kept}
+        assert not handles & seen, "a handle number was handed out twice"
+        seen |= handles
+        assert len(arena.accounting._keys) == len(arena.resident_keys())

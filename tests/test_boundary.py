@@ -9,7 +9,8 @@ call this build's Engine, pipeline and backend without changes.
 - QuailBackend.supports admits mi355x (the reference's allow-list,
   backend.py:333-344, is the gate this replaces);
 - KVArena.paged_kv gives the reference's (pages, 16, n_kv, d) views of the
-  MI355X pools, and layer_kv refuses to hand out the physical layout.
+  MI355X pools, and layer_kv row-indexed pools over the reference's flat
+  row numbering (reads and writes).
 """
 
 from types import SimpleNamespace
@@ -126,6 +127,14 @@ def test_execution_reports_missing_state_and_unknown_nodes():
         ex.execute(join, {"anchor_ids": [], "prefixes": [], "stage_suffixes": [[]]})
 
 
+def test_backend_plan_and_request_runner_raise_clearly():
+    backend = QuailBackend()
+    for call in (lambda: backend.plan(None, None), lambda: backend.prepare_request(None),
+                 lambda: backend.execute_request(None)):
+        with pytest.raises(NotImplementedError, match="start\\(GpuContext\\)"):
+            call()
+
+
 def test_paged_kv_views_match_the_reference_row_numbering():
     arena = KVArena(1, 6, 16, 2, 128, device="cpu")
     kp, vp = arena.page_pools(0)
@@ -138,8 +147,22 @@ def test_paged_kv_views_match_the_reference_row_numbering():
     for page, slot in ((0, 0), (3, 7), (5, 15)):
         assert torch.equal(kv[page, slot], k_rows[page * 16 + slot])
         assert torch.equal(vv[page, slot], v_rows[page * 16 + slot])
-    with pytest.raises(NotImplementedError, match="page_pools"):
-        arena.layer_kv(0)
+    # layer_kv: the reference's flat rows, read and written through the pages
+    kf, vf = arena.layer_kv(0)
+    assert kf.shape == (96, 2, 128) and vf.shape == (96, 2, 128) and len(kf) == 96
+    rows = torch.tensor([5, 17, 95, 40])
+    assert torch.equal(kf[rows], k_rows[rows]) and torch.equal(vf[rows], v_rows[rows])
+    assert torch.equal(kf[33], k_rows[33]) and torch.equal(vf[-1], v_rows[95])
+    assert torch.equal(vf[16:20], v_rows[16:20])
+    new_k = torch.randn(4, 2, 128).to(torch.bfloat16)
+    new_v = torch.randn(4, 2, 128).to(torch.bfloat16)
+    kf[rows] = new_k
+    vf[rows] = new_v
+    want_k, want_v = k_rows.clone(), v_rows.clone()
+    want_k[rows], want_v[rows] = new_k, new_v
+    assert torch.equal(layout.k_rows(kp), want_k) and torch.equal(layout.v_rows(vp), want_v)
+    with pytest.raises(IndexError):
+        kf[torch.tensor([96])]
 
 
 def test_backend_sizes_the_arena_with_the_reference_formula():

@@ -119,6 +119,26 @@ def test_e4m3_encoding_matches_torch_at_every_midpoint():
     assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8))
 
 
+def test_fused_epilogue_encoder_saturates_just_above_448():
+    """The fused epilogues' encoder has no +-448 clamp: a value no larger
+    than its group's amax gives |y / scale| <= 448 (1 + 2^-24), which fp32
+    rounds to at most 448 + 2^-15. Every value in (448, 464] must encode as
+    +-448 (0x7e / 0xfe), never as the NaN code, and values up to 448 as
+    torch's float8_e4m3fn cast does."""
+    above = torch.tensor([448 + 2 ** -15, 448 + 2 ** -10, 450.0, 455.5, 463.9, 464.0],
+                         dtype=torch.float32)
+    assert above[0].item() > 448 and above[0].item() == 448 + 2 ** -15
+    below = torch.tensor([448.0, 447.99, 440.0, 432.0, 0.0, 1.0, 2 ** -9, 2 ** -10],
+                         dtype=torch.float32)
+    x = torch.cat([above, -above, below, -below])
+    got = K.e4m3_encode(x.to(DEV)).cpu()
+    n = above.numel()
+    assert got[:n].tolist() == [0x7E] * n, [hex(v) for v in got[:n].tolist()]
+    assert got[n:2 * n].tolist() == [0xFE] * n, [hex(v) for v in got[n:2 * n].tolist()]
+    rest = x[2 * n:]
+    assert torch.equal(got[2 * n:], rest.to(torch.float8_e4m3fn).view(torch.uint8))
+
+
 def test_silu_mul_quant():
     g = _gen(3)
     T, I = 29, 9728
@@ -618,6 +638,15 @@ def test_gather_final_norm_and_answer_bits():
     clear = margin_ref.abs() > 0.05
     assert torch.equal(bits.cpu()[clear], bits_ref[clear])
     assert (margin.cpu() - margin_ref).abs().max().item() < 0.1
+    # AnswerRows.logits: the per-class maxima of the same bf16 scores
+    best_t, best_f = K.answer_logits(normed.to(DEV), w_ans.to(DEV), is_true.to(DEV))
+    assert best_t.dtype == torch.bfloat16 and best_t.shape == (64,)
+    assert torch.equal((best_t > best_f).to(torch.uint8).cpu(), bits.cpu())
+    assert torch.equal((best_t.float() - best_f.float()).cpu(), margin.cpu())
+    scores = normed.float() @ w_ans.float().t()
+    for got, cols in ((best_t, [0, 1, 2]), (best_f, [3, 4, 5])):
+        want = scores[:, cols].amax(dim=1)
+        assert ((got.cpu().float() - want).abs() <= want.abs() * 2 ** -7 + 1e-3).all()
 
 
 # The two tree kernels: "stream" (qh_tree_attention, node pages streamed
