@@ -651,40 +651,56 @@ class _Join:
 
     # ---- streamed anchors ------------------------------------------------
 
-    def admit(self, items):
-        arena = self.arena
+    def take(self, items):
+        """Anchors a source stream hands over, as (key, prefix) pairs with
+        their KV already resident: those the batch filter keeps join the
+        plan; the others' pages are freed at once."""
         if self.anchor_batch is not None and items:
-            kept = set(self.anchor_batch([key for key, _ in items]))
-            for key, _ in items:
-                if key not in kept and arena.is_resident(key):
-                    arena.free_key(key)
-            items = [(key, prefix) for key, prefix in items if key in kept]
+            wanted = set(self.anchor_batch([key for key, _ in items]))
+            dropped = [key for key, _ in items if key not in wanted]
+            for key in dropped:
+                if self.arena.is_resident(key):
+                    self.arena.free_key(key)
+            items = [item for item in items if item[0] in wanted]
         for key, prefix in items:
-            if not arena.is_resident(key):
-                raise ValueError(f"streamed anchor {key!r} has no KV in the arena")
-            arena.pin(key)
-            self.keys.append(key)
-            self.prefixes.append(prefix)
-            a = self.anchors.add(prefix)
-            got = self.sched.admit(self.anchors.length(a),
-                                   self.held_pages(key, self.anchors.length(a)),
-                                   partners=self.partners_of(key))
-            assert got == a, "anchor index out of step with its token table"
-            self.sched.set_key(a, arena.handle(key))
+            self.register(key, prefix)
 
-    def pull(self, evict_retained=False, force=False):
-        """Run source chunks until a join chunk can fill or the source blocks."""
-        moved = False
-        source = self.source
-        while not source.done and (force or self.sched.buildable_tokens() < self.budget):
-            force = False
-            before = source.chunks
-            items, blocked = source.next(evict_retained=evict_retained)
-            self.admit(items)
-            moved = moved or bool(items) or source.chunks > before
-            if blocked:
+    def register(self, key, prefix):
+        """One streamed anchor into the plan: pinned for the whole join, its
+        held pages priced, its partner lists looked up by key."""
+        if not self.arena.is_resident(key):
+            raise ValueError(f"streamed anchor {key!r} has no KV in the arena")
+        self.arena.pin(key)
+        self.keys.append(key)
+        self.prefixes.append(prefix)
+        index = self.anchors.add(prefix)
+        tokens = self.anchors.length(index)
+        planned = self.sched.admit(tokens, self.held_pages(key, tokens),
+                                   partners=self.partners_of(key))
+        assert planned == index, "anchor index out of step with its token table"
+        self.sched.set_key(index, self.arena.handle(key))
+
+    def source_active(self):
+        return self.source is not None and not self.source.done
+
+    def feed(self, may_evict=False, at_least_once=False):
+        """Let the anchor source run its chunks until the plan holds a full
+        join chunk of work or the source has to wait; with at_least_once
+        the source runs once even if the plan is full. Returns whether the
+        source launched a chunk or handed over an anchor."""
+        progressed = False
+        first = at_least_once
+        while self.source_active():
+            if not first and self.sched.buildable_tokens() >= self.budget:
                 break
-        return moved
+            first = False
+            launched = self.source.chunks
+            items, waiting = self.source.next(evict_retained=may_evict)
+            self.take(items)
+            progressed = progressed or bool(items) or self.source.chunks != launched
+            if waiting:
+                break
+        return progressed
 
     # ---- chunks ------------------------------------------------------------
 
@@ -731,23 +747,31 @@ class _Join:
                 layout.append((key, len(partners[1])))
         return layout
 
-    def run_part(self, part):
-        """Run one chunk of groups; on a full arena evict retained KV, else halve it."""
-        try:
-            self.run_one(part)
-        except ArenaFullError as error:
-            need = self.arena.page_cost(sum(self.entry_rows(*g) for g in part))
-            if self.arena.evict_retained(need):
-                logger.info("join chunk of %d groups retried after evicting retained KV",
-                            len(part))
-                self.run_part(part)
-                return
-            if len(part) < 2:
-                raise
-            logger.info("join chunk of %d groups split: %s", len(part), error)
-            half = len(part) // 2
-            self.run_part(part[:half])
-            self.run_part(part[half:])
+    def launch(self, groups):
+        """Run one admitted chunk. Admission prices the temporary pages of a
+        chunk's partner rows, but the packer claims them a page at a time,
+        so a chunk can still meet a full arena: then retained KV the size of
+        the chunk's rows is evicted and the chunk tried again, or, with
+        nothing left to evict, the chunk is split in two and the halves run
+        in order (each may split again)."""
+        stack = [list(groups)]
+        while stack:
+            part = stack.pop()
+            try:
+                self.run_one(part)
+            except ArenaFullError as error:
+                rows = sum(self.entry_rows(*g) for g in part)
+                if self.arena.evict_retained(self.arena.page_cost(rows)):
+                    logger.info("arena full for a join chunk of %d groups: retained KV "
+                                "evicted, chunk retried", len(part))
+                    stack.append(part)
+                elif len(part) > 1:
+                    logger.info("arena full for a join chunk of %d groups (%s): split "
+                                "in two", len(part), error)
+                    mid = len(part) // 2
+                    stack.extend((part[mid:], part[:mid]))
+                else:
+                    raise
 
     def run_one(self, part):
         torch, arena = self.torch, self.arena
@@ -781,53 +805,72 @@ class _Join:
             self.arena.free_key(key)
 
     def report(self, entry):
+        """Hand a finished chunk's answer rows to the plan, group by group. A
+        frame entry (the first group of an anchor's stage) leads with the
+        frame's own answer row, which answers nothing and is skipped."""
         groups, handle = entry
         bits = self.async_ans.result(handle)
-        pos = 0
+        first = 0
         for a, j, start, end, _ in groups:
-            if self.frames[j] and start == 0:
-                pos += 1          # the frame entry's answer row means nothing
-            for kind, anchor in self.sched.report(a, j, start, end, bits[pos:pos + end - start]):
+            if start == 0 and self.frames[j]:
+                first += 1
+            last = first + (end - start)
+            for kind, anchor in self.sched.report(a, j, start, end, bits[first:last]):
                 self.event(kind, anchor)
-            pos += end - start
+            first = last
 
     def run(self):
-        sched, arena, source = self.sched, self.arena, self.source
+        """Launch chunks until the plan and the anchor source are both done."""
         while True:
-            if source is not None and not source.done:
-                self.pull()
-            for kind, anchor in sched.take_settled():
+            if self.source_active():
+                self.feed()
+            # anchors with no partner at a stage settle without a chunk
+            for kind, anchor in self.sched.take_settled():
                 self.event(kind, anchor)
-            if sched.done() and (source is None or source.done):
+            if self.sched.done() and not self.source_active():
                 break
-            short = sched.blocked_pages
-            if short:
-                arena.evict_retained(short)
-            groups = sched.next_chunk(arena.free_pages)
+            groups = self.next_groups()
             if groups:
-                self.run_part(groups)
-                # packed children hold their parents' pages now
-                for a, _, start, _, carried in groups:
-                    parent = self.tree_parent[a] if a < len(self.tree_parent) else None
-                    if carried and start == 0 and parent is not None:
-                        arena.release(self.keys[parent])
-                continue
-            if self.outstanding:
-                self.report(self.outstanding.pop(0))
-                continue
-            if source is not None and not source.done and self.pull(evict_retained=True,
-                                                                   force=True):
-                continue
-            if sched.blocked_pages and arena.evict_retained(sched.blocked_pages):
-                continue
-            # parents held for queued children: the children pack whole
-            if arena.drop_holds(self.held):
-                continue
-            raise AssertionError("nothing buildable and nothing in flight")
+                self.launch(groups)
+                self.release_parents(groups)
+            elif not self.unstick():
+                raise AssertionError("no join chunk can be built and none is in flight")
         while self.outstanding:
             self.report(self.outstanding.pop(0))
-        arena.drop_holds(self.held)
-        arena.forget(self.keys)
+        self.arena.drop_holds(self.held)
+        self.arena.forget(self.keys)
+
+    def next_groups(self):
+        """The next chunk's groups; a fresh anchor short of pages first has
+        retained KV (which no anchor here reads) evicted for it."""
+        if self.sched.blocked_pages:
+            self.arena.evict_retained(self.sched.blocked_pages)
+        return self.sched.next_chunk(self.arena.free_pages)
+
+    def release_parents(self, groups):
+        """A child packed whole of its borrowed pages now holds them itself,
+        so its parent's hold for it ends."""
+        parents = self.tree_parent
+        for a, _, start, _, carried in groups:
+            parent = parents[a] if a < len(parents) else None
+            if carried and start == 0 and parent is not None:
+                self.arena.release(self.keys[parent])
+
+    def unstick(self):
+        """No chunk could be built: free something, in this order, and say
+        whether anything moved - read the oldest chunk in flight, let the
+        source run (evicting retained KV for its documents), evict retained
+        KV for the blocked anchor, or end the holds of parents kept for
+        children that then pack their whole prefixes."""
+        if self.outstanding:
+            self.report(self.outstanding.pop(0))
+            return True
+        if self.source_active() and self.feed(may_evict=True, at_least_once=True):
+            return True
+        short = self.sched.blocked_pages
+        if short and self.arena.evict_retained(short):
+            return True
+        return bool(self.arena.drop_holds(self.held))
 
 
 def run_join(torch, arena, pipeline, async_ans, anchor_prefixes, stage_suffixes, budget,

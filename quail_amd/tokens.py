@@ -24,6 +24,7 @@ tree fixes which pages every document reads:
 """
 
 import bisect
+import contextlib
 import os
 
 import numpy as np
@@ -302,69 +303,104 @@ class TokenLengths(_Rows):
         return np.concatenate(self.store._counts).astype(np.int64, copy=False)
 
 
-class _Writer:
-    """One Arrow IPC file written batch by batch; removed again on abort."""
+def _token_schema(list_type):
+    """The token store schema: ids and counts per document, tagged token_store."""
+    pa = _pa()
+    return pa.schema([pa.field(TokenStore.TOKEN_COLUMN, list_type, nullable=False),
+                      pa.field(TokenStore.COUNT_COLUMN, pa.int64(), nullable=False)],
+                     metadata={b"quail.kind": b"token_store"})
+
+
+def _token_arrays(documents, list_type):
+    """One record batch's columns for tokenized documents: the ids as one
+    large_list array built from offsets over the concatenated ids, and the
+    per-document counts."""
+    pa = _pa()
+    counts = np.fromiter(map(len, documents), dtype=np.int64, count=len(documents))
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    value_type = list_type.value_type
+    flat = np.empty(int(offsets[-1]), dtype=value_type.to_pandas_dtype())
+    for doc, lo, hi in zip(documents, offsets[:-1], offsets[1:]):
+        flat[lo:hi] = token_array(doc)
+    ids = pa.LargeListArray.from_arrays(pa.array(offsets), pa.array(flat, value_type))
+    return [ids, pa.array(counts)]
+
+
+class _IpcOutput:
+    """A new Arrow IPC file taking record batches of one schema.
+
+    seal() finishes the file (the footer makes it readable); discard()
+    finishes and deletes it. Each may be called more than once; only the
+    first call of either closes the file.
+    """
 
     def __init__(self, path, schema):
         pa = _pa()
         self.path = path
-        self._schema = schema
-        self._sink = pa.OSFile(path, "wb")
-        self._ipc = pa.ipc.new_file(self._sink, schema)
+        self.schema = schema
+        self._file = pa.OSFile(path, "wb")
+        self._batches = pa.ipc.new_file(self._file, schema)
+        self.sealed = False
 
-    def _write(self, arrays):
-        self._ipc.write_batch(_pa().RecordBatch.from_arrays(arrays, schema=self._schema))
+    def append(self, columns):
+        batch = _pa().RecordBatch.from_arrays(list(columns), schema=self.schema)
+        self._batches.write_batch(batch)
 
-    def _close(self):
-        self._ipc.close()
-        self._sink.close()
+    def seal(self):
+        if not self.sealed:
+            self.sealed = True
+            self._batches.close()
+            self._file.close()
 
-    def abort(self):
-        try:
-            self._close()
-        finally:
-            try:
-                os.unlink(self.path)
-            except FileNotFoundError:
-                pass
+    def discard(self):
+        self.seal()
+        if os.path.exists(self.path):
+            os.remove(self.path)
 
 
-class TokenStoreWriter(_Writer):
+@contextlib.contextmanager
+def _new_ipc_file(path, schema):
+    """`with _new_ipc_file(path, schema) as out:` appends batches to a new
+    file, sealed when the block ends and deleted if it raises, so a failed
+    write never leaves a partial store behind."""
+    out = _IpcOutput(path, schema)
+    try:
+        yield out
+    except BaseException:
+        out.discard()
+        raise
+    out.seal()
+
+
+class TokenStoreWriter:
     """Tokenize the document column of source batches into a token store
-    (tokens.py:193-229)."""
+    file, one record batch per source batch (tokens.py:193-229): the
+    streaming form the session's scan uses; TokenStore.write runs it over
+    a batch sequence."""
 
     def __init__(self, path, *, document_column, tokenizer, token_type):
-        pa = _pa()
-        self._column = document_column
-        self._tokenizer = tokenizer
-        self._list_type = pa.large_list(token_type)
-        schema = pa.schema(
-            [pa.field(TokenStore.TOKEN_COLUMN, self._list_type, nullable=False),
-             pa.field(TokenStore.COUNT_COLUMN, pa.int64(), nullable=False)],
-            metadata={b"quail.kind": b"token_store"})
-        super().__init__(path, schema)
+        self.path = path
+        self.document_column = document_column
+        self.tokenizer = tokenizer
+        self.list_type = _pa().large_list(token_type)
+        self._out = _IpcOutput(path, _token_schema(self.list_type))
 
     def write_tokens(self, documents):
         """Append one batch of already tokenized documents (sequences of ids)."""
-        pa = _pa()
-        value_type = self._list_type.value_type
-        lengths = np.fromiter((len(d) for d in documents), dtype=np.int64, count=len(documents))
-        offsets = np.zeros(len(documents) + 1, dtype=np.int64)
-        np.cumsum(lengths, out=offsets[1:])
-        parts = [token_array(d) for d in documents]
-        flat = (np.concatenate(parts) if parts else np.empty(0, np.int64)).astype(
-            value_type.to_pandas_dtype(), copy=False)
-        tokens = pa.LargeListArray.from_arrays(pa.array(offsets, pa.int64()),
-                                               pa.array(flat, value_type))
-        self._write([tokens, pa.array(lengths, pa.int64())])
+        self._out.append(_token_arrays(documents, self.list_type))
 
     def write_batch(self, batch):
         """Tokenize the document column of one source record batch."""
-        texts = batch.column(batch.schema.get_field_index(self._column))
-        self.write_tokens([self._tokenizer(t.as_py()) for t in texts])
+        texts = batch.column(self.document_column).to_pylist()
+        self.write_tokens([self.tokenizer(text) for text in texts])
+
+    def abort(self):
+        """Close and delete the partial file."""
+        self._out.discard()
 
     def finish(self):
-        self._close()
+        """Seal the file and open it as a TokenStore."""
+        self._out.seal()
         return TokenStore(self.path)
 
 
@@ -393,19 +429,22 @@ class TokenStore:
     @classmethod
     def write(cls, path, batches, *, document_column, tokenizer, token_type):
         """Tokenize bounded source batches into one file and open it."""
-        return _write_all(TokenStoreWriter(path, document_column=document_column,
-                                           tokenizer=tokenizer, token_type=token_type),
-                          batches, "write_batch")
+        list_type = _pa().large_list(token_type)
+        with _new_ipc_file(path, _token_schema(list_type)) as out:
+            for batch in batches:
+                texts = batch.column(document_column).to_pylist()
+                out.append(_token_arrays([tokenizer(t) for t in texts], list_type))
+        return cls(path)
 
     @classmethod
     def from_documents(cls, path, documents, *, token_type=None, batch_rows=4096):
         """Write already tokenized documents (sequences of ids), `batch_rows` per
         record batch, and open the file."""
-        token_type = _pa().int32() if token_type is None else token_type
-        writer = TokenStoreWriter(path, document_column=None, tokenizer=None,
-                                  token_type=token_type)
-        batches = [documents[i:i + batch_rows] for i in range(0, len(documents), batch_rows)]
-        return _write_all(writer, batches, "write_tokens")
+        list_type = _pa().large_list(_pa().int32() if token_type is None else token_type)
+        with _new_ipc_file(path, _token_schema(list_type)) as out:
+            for start in range(0, len(documents), batch_rows):
+                out.append(_token_arrays(documents[start:start + batch_rows], list_type))
+        return cls(path)
 
     @property
     def lengths(self):
@@ -435,62 +474,56 @@ class TokenStore:
         self._source.close()
 
 
-def _write_all(writer, batches, method):
-    try:
-        for batch in batches:
-            getattr(writer, method)(batch)
-    except BaseException:
-        writer.abort()
-        raise
-    return writer.finish()
-
-
-class ColumnStoreWriter(_Writer):
-    """Copy one source column into a column store file (tokens.py:232-251)."""
+class ColumnStoreWriter:
+    """Copy one source column into a column store file (tokens.py:232-251),
+    batch by batch; ColumnStore.write runs it over a batch sequence."""
 
     def __init__(self, path, field):
-        pa = _pa()
-        self._name = field.name
-        super().__init__(path, pa.schema([field], metadata={b"quail.kind": b"column_store"}))
+        self.path = path
+        self.name = field.name
+        self._out = _IpcOutput(path, _pa().schema(
+            [field], metadata={b"quail.kind": b"column_store"}))
 
     def write_batch(self, batch):
-        self._write([batch.column(batch.schema.get_field_index(self._name))])
+        self._out.append([batch.column(self.name)])
+
+    def abort(self):
+        self._out.discard()
 
     def finish(self):
-        self._close()
+        self._out.seal()
         return ColumnStore(self.path)
 
 
 class ColumnStore:
-    """One memory mapped source column kept for result rows (tokens.py:254-287)."""
+    """One source column kept for result rows (tokens.py:254-287): the file is
+    memory mapped and read as one table, so `values` is a chunked array over
+    the mapped buffers (one chunk per record batch), never a copy."""
 
     def __init__(self, path):
         pa = _pa()
         self.path = path
-        self._source = pa.memory_map(path, "r")
-        self._reader = pa.ipc.open_file(self._source)
-        self.name = self._reader.schema.names[0]
-        self._values = None
+        self._map = pa.memory_map(path, "r")
+        table = pa.ipc.open_file(self._map).read_all()
+        self.schema = table.schema
+        self.name = table.schema.names[0]
+        self.values = table.column(0)
 
     @classmethod
     def write(cls, path, batches, field):
-        return _write_all(ColumnStoreWriter(path, field), batches, "write_batch")
-
-    @property
-    def values(self):
-        if self._values is None:
-            pa = _pa()
-            self._values = pa.chunked_array(
-                [self._reader.get_batch(i).column(0)
-                 for i in range(self._reader.num_record_batches)],
-                type=self._reader.schema.field(0).type)
-        return self._values
+        """Copy one column of bounded input batches into a file and open it."""
+        schema = _pa().schema([field], metadata={b"quail.kind": b"column_store"})
+        with _new_ipc_file(path, schema) as out:
+            for batch in batches:
+                out.append([batch.column(field.name)])
+        return cls(path)
 
     def __len__(self):
         return len(self.values)
 
     def close(self):
-        self._source.close()
+        self.values = None
+        self._map.close()
 
 
 class TokenSelection(_Rows):

@@ -1,23 +1,18 @@
-"""pack_chunk and FilterAdmission against the reference's known answers.
+"""pack_chunk against the reference's known answers.
 
 pack_chunk literals: the plain-arena cases of the reference's
 tests/test_sliding_kv.py:216-297 (borrowing child under unified attention;
 siblings stacked under tree attention: cu_a == [0, 100, 101, 112, 119],
-reads cu_q == [0, 1, 19], used == [100, 64], max_q == 18). Admission
-literals: tests/test_pack.py:338-404 of the reference; random invariants
-in the style of tests/test_pack.py:211-250.
+reads cu_q == [0, 1, 19], used == [100, 64], max_q == 18). Filter
+admission's literal cases are data (tests/golden/admission_cases.json)
+and its invariants properties (test_admission_properties.py).
 """
 
-import random
-
-import numpy as np
 import pytest
 import torch
 
 from quail_amd import loop
 from quail_amd.arena import KVArena
-from quail_amd.pack import FilterAdmission, pages_for
-from quail_amd.tokens import PrefixTree
 
 
 def plain_arena(pages=64):
@@ -157,114 +152,3 @@ def test_arena_full_error_frees_the_temporaries_it_took():
         pack(arena, [dict(key=key, prefix=None, f=100, suffixes=[[1] * 10, [2] * 30])],
              "unified")
     assert arena.free_pages == 1
-
-
-def test_filter_admission_order_rewind_limits_and_whole_packing():
-    sched = FilterAdmission([100, 100], [10, 10], 200, arena_pages=100, page_tokens=16)
-    assert sched.next_chunk(100) == [(0, 0, True)]
-    sched.report(0, 0, True)
-    second = sched.next_chunk(100)
-    assert second[0] == (0, 1, False) and (1, 0, True) in second
-
-    sched = FilterAdmission([70, 60], [10], 200, arena_pages=7, page_tokens=16,
-                            kept_extra_tokens=30)
-    assert sched.next_chunk(7) == [(0, 0, True)]
-    assert sched.report(0, 0, True, release=False) == ()
-    assert 0 not in sched.resident
-    assert sched.next_chunk(5) == [] and sched.blocked_pages == 1
-    assert sched.next_chunk(6) == [(1, 0, True)]
-
-    with pytest.raises(ValueError):
-        FilterAdmission([1000], [10], 500, 100, 16)
-    with pytest.raises(ValueError):
-        FilterAdmission([64, 100], [1], 80, 100, 16,
-                        tree=PrefixTree([0, 1], [None, 0], [0, 48]))
-    with pytest.raises(ValueError):
-        FilterAdmission([64], [1], 80, None, 16, tree=PrefixTree([0], [None], [0]))
-    with pytest.raises(ValueError):
-        FilterAdmission([1000], [10], 2000, 2, 16)
-    sched = FilterAdmission([1000], [10], 2000, None, 16)
-    assert sched.next_chunk() == [(0, 0, True)]
-    assert sched.report(0, 0, False) == ()
-
-    sched = FilterAdmission([50, 50, 50], [10, 200], 250, arena_pages=100,
-                            page_tokens=16, limit=1)
-    for doc, _, _ in sched.next_chunk(100):
-        sched.report(doc, 0, True)
-    assert sched.next_chunk(100) == [(0, 1, False)]
-    sched.report(0, 1, True)
-    assert sched.done()
-    assert sched.drain_ready() == [1, 2]
-    assert not sched.resident
-
-    tree = PrefixTree(order=[0, 1], parent=[None, 0], shared=[0, 32])
-    sched = FilterAdmission([64, 64], [10], 200, arena_pages=20, page_tokens=16, tree=tree,
-                            can_borrow=lambda doc, parent, same_chunk: False)
-    assert sched.next_chunk(20) == [(0, 0, True), (1, 0, True)]
-    assert sched.borrowing.shared(1) == 0 and sched.own_tokens(1) == 64
-    # with borrowing allowed the child packs only its own tokens
-    sched = FilterAdmission([64, 64], [10], 200, arena_pages=20, page_tokens=16, tree=tree)
-    assert sched.next_chunk(20) == [(0, 0, True), (1, 0, True)]
-    assert sched.borrowing.shared(1) == 32 and sched.own_tokens(1) == 32
-
-
-def _drive(sched, truth, deliver_lag, arena_pages, rng):
-    chunks, outstanding = [], []
-    free = arena_pages
-    held = {}
-    while not sched.done():
-        groups = sched.next_chunk(free if arena_pages is not None else None)
-        if not groups:
-            assert outstanding, "stuck with nothing in flight"
-        for doc, stage, fresh in groups:
-            if fresh and arena_pages is not None:
-                need = pages_for(sched.doc_tokens[doc] - sched.borrowing.shared(doc)
-                                 + sched.kept_extra, 16)
-                held[doc] = need
-                free -= need
-        chunks.append(groups)
-        outstanding.append(groups)
-        while len(outstanding) > deliver_lag or (not groups and outstanding):
-            for doc, stage, _ in outstanding.pop(0):
-                for d in sched.report(doc, stage, bool(truth[doc][stage])):
-                    free += held.pop(d)
-            if not groups:
-                break
-    while outstanding:
-        for doc, stage, _ in outstanding.pop(0):
-            for d in sched.report(doc, stage, bool(truth[doc][stage])):
-                free += held.pop(d)
-    return chunks
-
-
-def test_filter_admission_invariants_over_random_shapes():
-    rng = random.Random(23)
-    for trial in range(30):
-        n_docs = rng.randrange(5, 60)
-        n_stages = 1 if trial % 3 == 0 else rng.randrange(1, 6)
-        doc_tokens = [rng.randrange(20, 900) for _ in range(n_docs)]
-        stage_tokens = [rng.randrange(10, 60) for _ in range(n_stages)]
-        budget = max(doc_tokens) + max(stage_tokens) + rng.randrange(0, 2000)
-        arena_pages = max(pages_for(max(doc_tokens), 16), rng.randrange(4, 200))
-        if trial % 3 == 0:
-            arena_pages = None
-        truth = [[1 if rng.random() < 0.7 else 0 for _ in range(n_stages)]
-                 for _ in range(n_docs)]
-        sched = FilterAdmission(doc_tokens, stage_tokens, budget, arena_pages, 16)
-        chunks = _drive(sched, truth, rng.choice((0, 1)), arena_pages, rng)
-        for groups in chunks:
-            tokens = sum((doc_tokens[d] if fresh else 0) + stage_tokens[s]
-                         for d, s, fresh in groups)
-            assert tokens <= budget
-            assert len({d for d, _, _ in groups}) == len(groups)
-        # every document answers up to its first FALSE
-        for d in range(n_docs):
-            want = []
-            for s in range(n_stages):
-                want.append(truth[d][s])
-                if not truth[d][s]:
-                    break
-            assert sched.answers[d] == want
-        # fresh admissions follow queue order among documents of equal treatment
-        fresh = [d for groups in chunks for d, _, f in groups if f]
-        assert sorted(fresh) == list(range(n_docs))

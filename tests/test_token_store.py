@@ -146,7 +146,9 @@ def test_column_store_round_trip(tmp_path):
     col = ColumnStore.write(str(tmp_path / "c.arrow"), batches, field)
     assert col.name == "title" and len(col) == 3
     assert col.values.to_pylist() == ["a", "bb", "ccc"]
-    assert col._reader.schema.metadata == {b"quail.kind": b"column_store"}
+    assert col.schema.metadata == {b"quail.kind": b"column_store"}
+    assert pa.ipc.open_file(str(tmp_path / "c.arrow")).schema.metadata == \
+        {b"quail.kind": b"column_store"}
 
 
 def test_writer_tokenizes_a_document_column(tmp_path):
@@ -155,6 +157,36 @@ def test_writer_tokenizes_a_document_column(tmp_path):
                              tokenizer=lambda s: [ord(ch) for ch in s],
                              token_type=pa.int32())
     assert [np.asarray(store[i]).tolist() for i in range(3)] == [[97, 98], [99], []]
+
+
+def test_streaming_writers_finish_and_abort(tmp_path):
+    """The session's route (quail/execution/session.py:473-501): one writer per
+    stored column, a batch at a time, finish() opening the store and abort()
+    removing the partial file."""
+    from quail_amd.tokens import ColumnStoreWriter, TokenStoreWriter
+    batches = [pa.RecordBatch.from_arrays([pa.array(["ab", ""]), pa.array([7, 8])],
+                                          names=["text", "n"]),
+               pa.RecordBatch.from_arrays([pa.array(["xyz"]), pa.array([9])],
+                                          names=["text", "n"])]
+    tw = TokenStoreWriter(str(tmp_path / "t.arrow"), document_column="text",
+                          tokenizer=lambda s: [ord(ch) for ch in s], token_type=pa.int64())
+    cw = ColumnStoreWriter(str(tmp_path / "n.arrow"), pa.field("n", pa.int64()))
+    for b in batches:
+        tw.write_batch(b)
+        cw.write_batch(b)
+    store, col = tw.finish(), cw.finish()
+    assert [np.asarray(store[i]).tolist() for i in range(3)] == [[97, 98], [], [120, 121, 122]]
+    assert store.lengths.numpy().tolist() == [2, 0, 3]
+    assert col.values.to_pylist() == [7, 8, 9] and col.values.num_chunks == 2
+    for cls, kw in ((TokenStoreWriter, dict(document_column="text", tokenizer=list,
+                                            token_type=pa.int32())),
+                    (ColumnStoreWriter, dict(field=pa.field("n", pa.int64())))):
+        path = str(tmp_path / "partial.arrow")
+        w = cls(path, **kw)
+        assert os.path.exists(path)
+        w.abort()
+        w.abort()
+        assert not os.path.exists(path)
 
 
 def test_failed_write_leaves_no_file(tmp_path):

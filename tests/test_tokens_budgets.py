@@ -1,51 +1,52 @@
 """Prefix tree and sizing formulas against the reference's known answers.
 
-prefix_tree: tests/test_tokens.py:74-108 of the reference and the worked
-example of docs/content/docs/architecture/prefix-caching.mdx:38-50.
+prefix_tree: the known answers of tests/test_tokens.py:74-108 of the
+reference and the worked example of docs/content/docs/architecture/
+prefix-caching.mdx:38-50, as data (tests/golden/prefix_tree_cases.json).
 Budgets: tests/test_specs_budgets.py:16-43 and tests/test_model_pipelines.py:
 45-58 of the reference, and the MI355X sizing they imply.
 """
 
+import json
+import os
 from dataclasses import replace
+
+import pytest
 
 from quail_amd import budgets
 from quail_amd.specs import H100_SXM, MI355X, QWEN3_4B_FP8, QWEN3_32B_FP8
 from quail_amd.tokens import DocumentPrefixes, prefix_tree
 
+HERE = os.path.dirname(os.path.abspath(__file__))
+TREE_CASES = json.load(open(os.path.join(HERE, "golden", "prefix_tree_cases.json")))["cases"]
 
-def test_prefix_tree_borrows_whole_pages_and_siblings_share_one_parent():
-    docs = [list(range(40)), list(range(50)), list(range(32)) + [99] * 20,
-            [7] * 20, [7] * 10]
+
+def _document(runs):
+    ids = []
+    for kind, x, y in runs:
+        ids.extend(range(x, y) if kind == "range" else [x] * y)
+    return ids
+
+
+@pytest.mark.parametrize("case", TREE_CASES, ids=[c["name"] for c in TREE_CASES])
+def test_prefix_tree_known_answers(case):
+    docs = [_document(runs) for runs in case["documents"]]
+    tree = prefix_tree(docs, case["page_tokens"])
+    for field in ("order", "parent", "shared", "shared_tokens"):
+        if field in case:
+            assert getattr(tree, field) == case[field], (case["name"], field)
+    # parents come before their children in the order
+    first = {doc: i for i, doc in enumerate(tree.order)}
+    assert all(p is None or first[p] < first[d] for d, p in enumerate(tree.parent))
+
+
+def test_worked_example_computes_each_token_once():
+    """prefix-caching.mdx:38-50: three traces of one log, 1,000 / 1,400 /
+    1,900 tokens, compute 1,000 + 408 + 508 tokens with borrowing."""
+    case = next(c for c in TREE_CASES if c["name"] == "docs_worked_example")
+    docs = [_document(runs) for runs in case["documents"]]
     tree = prefix_tree(docs, 16)
-    assert tree.order == [0, 1, 2, 4, 3]
-    assert tree.parent == [None, 0, 0, None, None]
-    assert tree.shared == [0, 32, 32, 0, 0]
-    assert tree.shared_tokens == 64
-    first = {index: pos for pos, index in enumerate(tree.order)}
-    assert all(p is None or first[p] < first[i] for i, p in enumerate(tree.parent))
-    assert prefix_tree([], 16).shared_tokens == 0
-    tree = prefix_tree([[], [], [5] * 16 + [6]], 16)
-    assert tree.parent == [None, None, None] and tree.shared == [0, 0, 0]
-
-    header = list(range(64))
-    docs = [header + [1] * 8, header + [2] * 8, header + [3] * 8,
-            header + [3] * 8 + [4] * 40, header + [5] * 8]
-    tree = prefix_tree(docs, 16)
-    assert tree.parent == [None, 0, 0, 0, 0]
-    assert tree.shared == [0, 64, 64, 64, 64]
-    docs = [header + [1] * 32, header + [1] * 32 + [2] * 8, header + [1] * 32 + [3] * 8]
-    tree = prefix_tree(docs, 16)
-    assert tree.parent == [None, 0, 0] and tree.shared == [0, 96, 96]
-
-
-def test_prefix_tree_docs_worked_example():
-    trace = list(range(2000))
-    tree = prefix_tree([trace[:1000], trace[:1400], trace[:1900]], 16)
-    assert tree.order == [0, 1, 2]
-    assert tree.parent == [None, 0, 1]
-    assert tree.shared == [0, 992, 1392]
-    computed = sum(n - s for n, s in zip((1000, 1400, 1900), tree.shared))
-    assert computed == 1000 + 408 + 508 == 1916
+    assert sum(len(d) - s for d, s in zip(docs, tree.shared)) == 1000 + 408 + 508
 
 
 def test_prefix_tree_sorts_ids_as_big_endian_int32():
