@@ -117,3 +117,49 @@ def tiny_join(seed, n_anchors, n_partners, root=40, max_doc=60, frame_len=5, voc
     frame = rng.integers(0, vocab, size=frame_len)
     partners = [rng.integers(0, vocab, size=int(rng.integers(2, 30))) for _ in range(n_partners)]
     return anchors, frame, partners
+
+
+def decision_stats(gpu, ref, alt):
+    """Decision parity of a GPU run against the oracle, measured against the
+    oracle's own floor. Each argument is (bits, margins), dicts or lists by
+    row; ref is the fp64 oracle, alt the fp32 oracle.
+
+    The oracle pair's margin shift |alt - ref| is the noise any change of
+    accumulation order makes on this model. Its 99th percentile is the
+    band: a row whose fp64 margin lies beyond it is decided by the
+    algorithm, not by rounding, to 99 % confidence per row; beyond twice
+    the band, by a wide margin. Returns a dict of counts and shifts."""
+    n = len(ref[0])
+    rows = range(n)
+    rb, rm = [ref[0][d] for d in rows], np.array([ref[1][d] for d in rows])
+    ab, am = [alt[0][d] for d in rows], np.array([alt[1][d] for d in rows])
+    gb, gm = [gpu[0][d] for d in rows], np.array([gpu[1][d] for d in rows])
+    oracle_shift = np.abs(am - rm)
+    gpu_shift = np.abs(gm - rm)
+    band = float(np.quantile(oracle_shift, 0.99))
+    out = {"rows": n, "band": band,
+           "gpu_agree": sum(g == r for g, r in zip(gb, rb)),
+           "floor": sum(a == r for a, r in zip(ab, rb)),
+           "median_margin": float(np.median(np.abs(rm))),
+           "oracle_shift_median": float(np.median(oracle_shift)),
+           "gpu_shift_median": float(np.median(gpu_shift)),
+           "oracle_shift_p90": float(np.quantile(oracle_shift, 0.9)),
+           "gpu_shift_p90": float(np.quantile(gpu_shift, 0.9))}
+    for name, width in (("band", band), ("wide", 2 * band)):
+        clear = [d for d in rows if abs(rm[d]) > width]
+        out[f"outside_{name}"] = len(clear)
+        out[f"gpu_agree_{name}"] = sum(gb[d] == rb[d] for d in clear)
+        out[f"floor_{name}"] = sum(ab[d] == rb[d] for d in clear)
+    out["disagree_margins"] = sorted(round(float(rm[d]), 4) for d in rows if gb[d] != rb[d])
+    return out
+
+
+def describe(stats):
+    s = stats
+    return (f"{s['rows']} rows: GPU-vs-fp64 {s['gpu_agree']}, fp32-vs-fp64 {s['floor']}; "
+            f"band (p99 of the oracle pair's margin shift) {s['band']:.4f}: outside it "
+            f"{s['outside_band']} rows, GPU agrees on {s['gpu_agree_band']}, fp32 on "
+            f"{s['floor_band']}; outside twice it {s['outside_wide']} rows, GPU agrees on "
+            f"{s['gpu_agree_wide']}; margin shift median / p90 GPU {s['gpu_shift_median']:.4f}"
+            f" / {s['gpu_shift_p90']:.4f}, oracle pair {s['oracle_shift_median']:.4f} / "
+            f"{s['oracle_shift_p90']:.4f}; median |margin| {s['median_margin']:.4f}")

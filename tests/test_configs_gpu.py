@@ -569,10 +569,12 @@ def _oracle_stage_engine(stage):
     gemm      the four projections as exact fp64 block sums rounded to bf16
               (ops.fp8_gemm), the q/k norm, rotary and SiLU quant on the
               kernels that follow the plain GEMM;
-    attention the paged causal attention in fp32 (ops.paged_attention)
-              over the arena's pages (read through KVArena.layer_kv), its
-              bf16 output quantized by the group-quant kernel (the oracle
-              quantizes the same bf16 values);
+    attention the unified path's paged causal attention in fp32
+              (ops.paged_attention) over the arena's pages (read through
+              KVArena.layer_kv), or the tree path's call A + call B + bf16
+              LSE merge (ops.varlen_attention, paged_attention,
+              merge_attn); the bf16 output quantized by the group-quant
+              kernel (the oracle quantizes the same bf16 values);
     norm      the input / post-attention RMSNorm + quant, the q/k norm +
               rotary, the SiLU + quant and the final norm as the oracle's
               torch functions (ops.norm_quant_plain, add_rms_norm_quant,
@@ -637,6 +639,29 @@ def _oracle_stage_engine(stage):
             out, _ = ref.fused_add_rms_norm(hidden[rows], residual[rows], norm.weight,
                                             norm.variance_epsilon)
             return out
+
+        def attention_tree(self, q3, k3, v3, meta):
+            if stage != "attention":
+                return super().attention_tree(q3, k3, v3, meta)
+            # call A over the chunk's own segments, call B over the reads,
+            # the bf16 LSE merge (the oracle's tree layer step)
+            layer, reads = meta["layer"], meta["reads"]
+            n = q3.shape[0]
+            k_pool, v_pool = self.arena.page_pools(layer)
+            if meta["kv_src"] is not None:
+                K.kv_row_scatter(k3, v3, k_pool, v_pool, meta["kv_src"], meta["kv_dst"])
+            out_a, lse_a = ref.varlen_attention(q3, k3, v3, meta["cu_a"].cpu(),
+                                                self.softmax_scale, causal=True)
+            out = out_a.to(torch.bfloat16)
+            if reads is not None:
+                k_rows, v_rows = self.arena.layer_kv(layer)
+                out_b, lse_b = ref.paged_attention(
+                    q3, k_rows, v_rows, reads["cu_q"].cpu(), reads["used"].cpu(),
+                    reads["table"].cpu(), self.softmax_scale, False, q_rows=reads["rows"].cpu())
+                out = ref.merge_attn(out, lse_a, out_b.to(torch.bfloat16), lse_b,
+                                     reads["source"]).to(torch.bfloat16)
+            meta["layer"] += 1
+            return K.group_quant(out.reshape(n, -1), self.use_ue8m0)
 
         def _unified_fp8(self, q3, k3, v3, meta):
             if stage != "attention" or meta["unified"] is None:
@@ -732,36 +757,30 @@ def test_qwen3_4b_decisions_oracle_replay(form, part):
 
 def test_qwen3_4b_decisions_over_1024_rows_agree_within_the_oracle_floor():
     """The two oracle forms are equally valid restatements of the reference's
-    arithmetic, so where they disagree the decision is not determined by
-    the algorithm: on a random-init model, 36 layers of dynamic 1x128 fp8
-    re-quantization make such rows common. The bars: every row the GPU
-    decides differently from the fp64 oracle lies inside the noise band
-    (twice the largest oracle-vs-oracle margin shift), i.e. 0 disagreements
-    outside it; and the GPU agrees with the fp64 oracle as often as the
-    fp32 oracle does, within three binomial standard deviations."""
-    import numpy as np
+    arithmetic; their margin shift |fp32 - fp64| measures the noise any
+    change of accumulation order makes on this random-init model (36
+    layers of dynamic 1x128 fp8 re-quantization). The band is that shift's
+    99th percentile. Bars: beyond twice the band the GPU decides every row
+    as the fp64 oracle does; beyond the band it agrees on at least 98 % of
+    rows; its median margin shift is at most 1.5 times the oracle pair's
+    (the GPU has three families of rounding differences - GEMM block sums,
+    attention's bf16 P and output, norm summation orders - where the pair
+    has one); and its overall agreement is within three binomial standard
+    deviations of the pair's. Taking any one of those families from the
+    oracle instead leaves the agreement within a few rows of the GPU's
+    (a builder run: GEMMs 913, attention 919, norms 920 against the GPU's
+    915 of 1,024), so no single stage dominates."""
+    from e2e_support import decision_stats, describe
 
     st = _decision_gpu_run()
     assert set(st["runs"]) == set(DECIDE_PARTS), "run the replay parts first"
     n = DECIDE_ROWS
-    answers, margins = st["answers"], st["margins"]
-    (ref_bits, ref_m), (alt_bits, alt_m) = st["runs"]["fp64"], st["runs"]["fp32"]
-    shift = max(abs(ref_m[d] - alt_m[d]) for d in range(n))
-    band = 2 * shift
-    floor = sum(ref_bits[d] == alt_bits[d] for d in range(n))
-    agree = sum(answers[d] == ref_bits[d] for d in range(n))
-    agree_alt = sum(answers[d] == alt_bits[d] for d in range(n))
-    outside = [d for d in range(n) if answers[d] != ref_bits[d] and abs(ref_m[d]) > band]
-    clear = [d for d in range(n) if abs(ref_m[d]) > band]
-    clear_agree = sum(answers[d] == ref_bits[d] for d in clear)
-    gpu_shift = max(abs(margins[d] - ref_m[d]) for d in range(n))
-    typical = float(np.median([abs(ref_m[d]) for d in range(n)]))
-    print(f"{n} rows: GPU-vs-fp64 {agree}/{n} ({100 * agree / n:.1f} %), GPU-vs-fp32 "
-          f"{agree_alt}/{n}, fp64-vs-fp32 {floor}/{n} ({100 * floor / n:.1f} %); noise band "
-          f"{band:.4f} (largest oracle shift {shift:.4f}, GPU shift {gpu_shift:.4f}, median "
-          f"|margin| {typical:.4f}); rows outside the band {len(clear)}, GPU agrees on "
-          f"{clear_agree}; disagreements outside the band {len(outside)}", flush=True)
-    assert not outside, f"rows decided differently outside the noise band: {outside[:10]}"
-    q = 1.0 - floor / n
+    gpu = (st["answers"], st["margins"])
+    stats = decision_stats(gpu, st["runs"]["fp64"], st["runs"]["fp32"])
+    print(describe(stats), flush=True)
+    assert stats["gpu_agree_wide"] == stats["outside_wide"], stats["disagree_margins"]
+    assert stats["gpu_agree_band"] >= 0.98 * stats["outside_band"], stats
+    assert stats["gpu_shift_median"] <= 1.5 * stats["oracle_shift_median"], stats
+    q = 1.0 - stats["floor"] / n
     slack = 3.0 * (2.0 * n * q * (1.0 - q)) ** 0.5
-    assert agree >= floor - slack, f"GPU agrees on {agree}/{n}, the oracles on {floor}/{n}"
+    assert stats["gpu_agree"] >= stats["floor"] - slack, stats

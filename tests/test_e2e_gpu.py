@@ -16,9 +16,11 @@ output). The bars, written in the tests:
   - teacher-forced per layer (the oracle layer gets the GPU's layer input,
     so drift cannot cascade across layers): down-projection output within
     8% relative L2 (worst row 20%), residual stream within 2%;
-  - decisions: every row decided differently lies inside the noise band
-    (twice the largest margin shift between the two oracle forms), and at
-    least 90% of all rows agree (a gross-failure bound).
+  - decisions, against the noise of the two oracle forms measured in the
+    same test: every row whose margin lies beyond twice the 99th
+    percentile of the oracles' margin shift is decided as the oracle
+    decides it, the GPU's margins move at most twice as far, and it
+    disagrees on at most about twice as many rows as the oracles do.
 """
 
 from dataclasses import replace
@@ -27,7 +29,8 @@ import numpy as np
 import pytest
 import torch
 
-from e2e_support import (TINY, TINY_FALSE, TINY_TRUE, gpu_filter, tiny_workload)
+from e2e_support import (TINY, TINY_FALSE, TINY_TRUE, decision_stats, describe, gpu_filter,
+                         tiny_workload)
 from oracle import forward as oforward
 from quail_amd import loop
 from quail_amd.arena import KVArena
@@ -148,8 +151,8 @@ def test_qwen3_32b_geometry_layers_match_the_oracle(path):
 def test_decisions_agree_outside_the_noise_band(path):
     model = build_random_qwen3(TINY, seed=3, device="cuda", max_pos=2048,
                                answer_token_ids=TINY_TRUE + TINY_FALSE)
-    docs, tail = tiny_workload(seed=4, n_rows=96)
-    pages = 400
+    docs, tail = tiny_workload(seed=4, n_rows=400)
+    pages = 400 * 14 + 64
     answers, margins, records, stream = gpu_filter(
         model, TINY, docs, tail, path=path, pages=pages, budget=2000,
         true_ids=TINY_TRUE, false_ids=TINY_FALSE)
@@ -167,23 +170,23 @@ def test_decisions_agree_outside_the_noise_band(path):
                                                b2.tolist(), m2.tolist()):
             ref_bits[doc], ref_margin[doc], alt_bits[doc], alt_margin[doc] = x1, y1, x2, y2
     n = len(docs)
-    shift = max(abs(ref_margin[d] - alt_margin[d]) for d in range(n))
-    floor = sum(ref_bits[d] == alt_bits[d] for d in range(n))
-    agree = sum(answers[d] == ref_bits[d] for d in range(n))
-    band = 2 * shift
-    off = sorted(round(ref_margin[d], 4) for d in range(n) if answers[d] != ref_bits[d])
-    print(f"{path}: GPU-vs-oracle {agree}/{n}, oracle-vs-oracle {floor}/{n}, "
-          f"largest oracle-vs-oracle margin shift {shift:.4f} (noise band {band:.4f}); "
-          f"oracle margins of the rows decided differently {off}", flush=True)
-    # the bar is the oracles' own noise: every row decided differently lies
-    # inside twice the largest margin shift between the two oracle forms;
-    # the count bound only catches a gross failure (a broken kernel agrees
-    # on about half of the rows)
-    for d in range(n):
-        if answers[d] != ref_bits[d]:
-            assert abs(ref_margin[d]) <= band, \
-                f"row {d}: decision differs at margin {ref_margin[d]:.4f} (band {band:.4f})"
-    assert agree >= 0.9 * n, f"GPU agrees on {agree}/{n}"
+    stats = decision_stats((answers, margins), (ref_bits, ref_margin), (alt_bits, alt_margin))
+    print(f"{path}: {describe(stats)}; oracle margins of the rows decided differently "
+          f"{stats['disagree_margins']}", flush=True)
+    # the bars are the oracle pair's own noise, measured here: every row whose
+    # fp64 margin lies beyond twice the 99th-percentile oracle shift is
+    # decided as the oracle decides it; the GPU's margins move at most 2.5
+    # times as far as the oracle pair's (median; measured 1.8-1.85: the GPU
+    # differs from the fp64 oracle in GEMM block sums, attention's bf16
+    # roundings and norm summation orders, the fp32 oracle in GEMM order
+    # only, and taking any one of the three from the oracle leaves the
+    # shift within 0.035-0.049 against the GPU's 0.039); and it disagrees
+    # with the fp64 oracle on at most twice as many rows as the fp32 oracle
+    # does, plus three Poisson standard deviations of that count
+    assert stats["gpu_agree_wide"] == stats["outside_wide"], stats
+    assert stats["gpu_shift_median"] <= 2.5 * stats["oracle_shift_median"] + 1e-3, stats
+    pair = n - stats["floor"]
+    assert n - stats["gpu_agree"] <= 2 * pair + 3.0 * max(1.0, (2 * pair) ** 0.5), stats
 
 
 def test_ue8m0_mode_runs_the_mfma_scaled_gemms_and_agrees_with_the_oracle():
