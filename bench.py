@@ -30,8 +30,6 @@ FP8_PEAK_TFLOPS = 5033.2     # MI355X dense fp8 MFMA (AMD published)
 BF16_PEAK_TFLOPS = 2516.6    # MI355X dense bf16 MFMA
 HBM_PEAK_GBPS = 8000.0
 PEAK_CLOCK_GHZ = 2.4         # the clock the published MFMA peaks assume
-GEMM_CLOCK_GHZ = 1.85        # the fp8 GEMMs' shader clock on the AI.IF filter (GRBM counters)
-ATTN_CLOCK_GHZ = 2.08        # the paged attention kernel's shader clock there (same counters)
 
 
 def host_cpu():
@@ -216,6 +214,41 @@ def copy_calibration(nbytes):
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_fp8_aiif_qwen3_4b_hbm_traffic.md")
 
 
+CLOCK_PROFILE = os.path.join(ROOT, "profiles", "gpu_clock_aiif_qwen3_4b_1024rows.md")
+
+
+def profiled_clocks():
+    """The shader clocks (GHz) the fp8 GEMMs and the paged attention kernel held
+    on the AI.IF filter, from the committed GRBM clock-counter profile of this
+    workload: GEMM = dispatch-time-weighted mean over the fp8_gemm_kernel rows.
+    Returns (gemm, attention, source) or (None, None, reason); the clock is
+    not measured by this run."""
+    import re
+    try:
+        with open(CLOCK_PROFILE) as f:
+            text = f.read()
+    except OSError:
+        return None, None, "no clock profile"
+    gemm_w = gemm_t = 0.0
+    attn = None
+    for line in text.splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) < 4:
+            continue
+        try:
+            n, us, mhz = int(cells[1]), float(cells[2]), float(cells[3])
+        except ValueError:
+            continue
+        if "fp8_gemm_kernel" in cells[0]:
+            gemm_w += n * us * mhz
+            gemm_t += n * us
+        elif re.search(r"attn_paged_kernel<true, true>", cells[0]):
+            attn = mhz / 1e3
+    if not gemm_t:
+        return None, None, "clock profile has no fp8_gemm_kernel rows"
+    return gemm_w / gemm_t / 1e3, attn, os.path.relpath(CLOCK_PROFILE, ROOT)
+
+
 def measured_gemm_traffic():
     """(bytes per launch, source) from the committed counter profile, or (None, reason)."""
     import re
@@ -379,6 +412,8 @@ def main():
         traffic, traffic_src = None, "not measured for this workload"
     else:
         traffic, traffic_src = measured_gemm_traffic()
+    gemm_clk, attn_clk, clk_src = ((None, None, "not profiled for this workload") if big
+                                   else profiled_clocks())
     line = {
         "metric": (f"rows/s + prefill tok/s, {'Qwen3-32B' if big else 'Qwen3-4B'} fp8 AI.IF "
                    f"on 1 GPU; attn/GEMM % of MFMA peak"),
@@ -412,20 +447,21 @@ def main():
                      "algorithmic_bytes_per_launch": round(k["gemm_bytes"] / max(1, k["gemm_launches"])),
                      "kernel": ("qh fp8_gemm_kernel: qkv, o, down (bf16 out) and gate_up "
                                 "(fused SiLU gate + fp8 quant epilogue)"),
-                     # the published peak assumes 2.4 GHz; the GEMMs hold ~1.85 GHz on this
-                     # workload (GRBM clock counters, profiles/gpu_clock_aiif_qwen3_4b_1024rows.md)
-                     "at_measured_clock": {
-                         "clock_ghz": GEMM_CLOCK_GHZ,
-                         "peak": round(FP8_PEAK_TFLOPS * GEMM_CLOCK_GHZ / PEAK_CLOCK_GHZ, 1),
-                         "frac": round(k["gemm_tflops"] / (FP8_PEAK_TFLOPS * GEMM_CLOCK_GHZ
+                     # the published peak assumes 2.4 GHz; the GEMMs' clock on this workload
+                     # comes from the committed GRBM clock-counter profile (not this run)
+                     "at_profiled_clock": None if gemm_clk is None else {
+                         "clock_ghz": round(gemm_clk, 3),
+                         "peak": round(FP8_PEAK_TFLOPS * gemm_clk / PEAK_CLOCK_GHZ, 1),
+                         "frac": round(k["gemm_tflops"] / (FP8_PEAK_TFLOPS * gemm_clk
                                                            / PEAK_CLOCK_GHZ), 4),
-                         "source": "profiles/gpu_clock_aiif_qwen3_4b_1024rows.md"}},
+                         "source": clk_src}},
         "gemm": {"share_of_step": round(k["gemm_ms"] / (ms_per_step * args.steps), 3),
                  "shapes": k["gemm_shapes"]},
         "attention": {"tflops": round(k["attn_tflops"], 1),
                       "frac_bf16_peak": round(k["attn_tflops"] / BF16_PEAK_TFLOPS, 4),
-                      "frac_bf16_peak_at_measured_clock": round(
-                          k["attn_tflops"] / (BF16_PEAK_TFLOPS * ATTN_CLOCK_GHZ / PEAK_CLOCK_GHZ), 4),
+                      "frac_bf16_peak_at_profiled_clock": None if attn_clk is None else round(
+                          k["attn_tflops"] / (BF16_PEAK_TFLOPS * attn_clk / PEAK_CLOCK_GHZ), 4),
+                      "profiled_clock_ghz": None if attn_clk is None else round(attn_clk, 3),
                       "gather_gbps": round(k["attn_gbps"], 1),
                       "gather_frac_hbm": round(k["attn_gbps"] / HBM_PEAK_GBPS, 4),
                       "share_of_step": round(k["attn_ms"] / (ms_per_step * args.steps), 3),

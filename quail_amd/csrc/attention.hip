@@ -1236,7 +1236,9 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
         amax = fmaxf(amax, fabsf(v1));
       }
     amax = xor32_max(amax);
-    const float scale = group_scale(amax, p.ue8m0 != 0);
+    // the output parameters, read here (late_params: not held across the loop)
+    const auto* E = late_params<TreeParams>();
+    const float scale = group_scale(amax, E->ue8m0 != 0);
     const double rinv = recip_exact(scale);
     uint32_t w[4][4];
 #pragma unroll
@@ -1249,13 +1251,14 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
     // before the stages become staging rows
     wg_barrier();
     store_fp8_rows(lds + wave * 32 * 144, w, lane,
-                   p.out_q + (long)(q0 + i0) * p.ld_out_q + (long)hq * D, p.ld_out_q,
+                   E->out_q + (long)(q0 + i0) * E->ld_out_q + (long)hq * D, E->ld_out_q,
                    count - i0);
     if (my_i >= count) return;
-    if (half == 0) p.out_scales[(long)hq * p.n_rows + qi] = scale;
+    if (half == 0) E->out_scales[(long)hq * E->n_rows + qi] = scale;
   } else {
     if (my_i >= count) return;
-    uint16_t* op = p.out + qi * p.ldo + (long)hq * D;
+    const auto* E = late_params<TreeParams>();
+    uint16_t* op = E->out + qi * E->ldo + (long)hq * D;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -1670,7 +1673,9 @@ __global__ __launch_bounds__(512, 1) void attn_tree_node_kernel(TreeParams p) {
           amax = fmaxf(amax, fabsf(v1));
         }
       amax = xor32_max(amax);
-      const float scale = group_scale(amax, p.ue8m0 != 0);
+      // the output parameters, read here (late_params: not held across the loop)
+      const auto* E = late_params<TreeParams>();
+      const float scale = group_scale(amax, E->ue8m0 != 0);
       const double rinv = recip_exact(scale);
       uint32_t w[4][4];
 #pragma unroll
@@ -1679,21 +1684,21 @@ __global__ __launch_bounds__(512, 1) void attn_tree_node_kernel(TreeParams p) {
         for (int g = 0; g < 4; ++g)
           w[db][g] = quant_e4m3_x4(acc_o[db][4 * g], acc_o[db][4 * g + 1], acc_o[db][4 * g + 2],
                                    acc_o[db][4 * g + 3], rinv);
+      uint8_t* const out_rows = E->out_q + (long)(q0 + i0w) * E->ld_out_q + (long)hq * D;
       // the ring holds the staging rows of 4 waves at a time
       if (rh == 0)
-        store_fp8_rows(lds + RES * STAGE + (wave & 3) * 32 * 144, w, lane,
-                       p.out_q + (long)(q0 + i0w) * p.ld_out_q + (long)hq * D, p.ld_out_q,
-                       count - i0w);
+        store_fp8_rows(lds + RES * STAGE + (wave & 3) * 32 * 144, w, lane, out_rows,
+                       E->ld_out_q, count - i0w);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       wg_barrier();
       if (rh == 1)
-        store_fp8_rows(lds + RES * STAGE + (wave & 3) * 32 * 144, w, lane,
-                       p.out_q + (long)(q0 + i0w) * p.ld_out_q + (long)hq * D, p.ld_out_q,
-                       count - i0w);
-      if (my_i < count && half == 0) p.out_scales[(long)hq * p.n_rows + qi] = scale;
+        store_fp8_rows(lds + RES * STAGE + (wave & 3) * 32 * 144, w, lane, out_rows,
+                       E->ld_out_q, count - i0w);
+      if (my_i < count && half == 0) E->out_scales[(long)hq * E->n_rows + qi] = scale;
     } else {
       if (my_i < count) {
-        uint16_t* op = p.out + qi * p.ldo + (long)hq * D;
+        const auto* E = late_params<TreeParams>();
+        uint16_t* op = E->out + qi * E->ldo + (long)hq * D;
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll

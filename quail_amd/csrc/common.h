@@ -111,6 +111,19 @@ __device__ __forceinline__ void wg_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// The kernel's by-value parameter block read through the kernarg segment at
+// the point of use. The empty asm makes the pointer opaque, so the compiler
+// cannot hoist these scalar loads to the kernel's start: parameters used only
+// after a long loop (epilogue outputs) then hold no scalar registers across
+// it, which left to the compiler spilled scalars into VGPR lanes.
+template <typename P>
+__device__ __forceinline__ const __attribute__((address_space(4))) P* late_params() {
+  const __attribute__((address_space(4))) uint8_t* ka =
+      (const __attribute__((address_space(4))) uint8_t*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(ka));
+  return reinterpret_cast<const __attribute__((address_space(4))) P*>(ka);
+}
+
 // Two values rounded to bf16 by one v_cvt_pk_bf16_f32 and widened back to
 // fp32: the same bits as round_bf16 on each.
 __device__ __forceinline__ void round_bf16_pair(float& a, float& b) {
