@@ -705,6 +705,13 @@ def attention_bench(args):
                                torch.tensor([prefix], dtype=torch.int32), scale)
     cpu_s = time.perf_counter() - t0
     err = (got - want).abs().max().item()
+    # the unified path computes the same function (prefix pages + own pages,
+    # bottom-right causal): its bf16 output against the same oracle
+    K.kv_row_scatter(kd, vd, kp, vp, src_d, dst_d)
+    got_u = K.attention(qd, cu_d, used_u, n_queries=T, max_q=int(suf.max()),
+                        softmax_scale=scale, causal=True, k_pool=kp, v_pool=vp, table=tab_u,
+                        n_kv=n_kv)[0].float().cpu()
+    err_u = (got_u - want).abs().max().item()
     if not args.no_cpu_baseline:
         cpu = {"value": round(flops / cpu_s / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
                "cpu_model": cpu_model, "kind": "port",
@@ -728,6 +735,7 @@ def attention_bench(args):
                      "kernel": "qh attn_tree_kernel (fused node + own rows, fp8 out)"},
         "paths": results,
         "parity_max_abs_vs_oracle": round(err, 6),
+        "unified_parity_max_abs_vs_oracle": round(err_u, 6),
         "tree_resident_bit_identical": same_bits,
         "cpu_baseline": cpu,
     }

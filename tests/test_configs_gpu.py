@@ -15,6 +15,9 @@
   (those that attend the most keys), and the fused tree kernel over a
   3,072-key node with 1,024-row own segments against the fp32 oracle run
   on the GPU.
+- the prefix-shared attention layer at its own shape (64 rows x 256-token
+  prefix, 32/8 heads): unified, tree and two-pass paths against the fp32
+  oracle.
 - one chunk packed at the full Qwen3-4B filter budget (110,376 tokens)
   through every stage of one layer, each stage against the oracle on the
   GPU's own input to it.
@@ -197,6 +200,142 @@ def test_tree_attention_over_a_3072_key_node_at_32b_geometry():
     print(f"tree 32B geometry, node {node} keys + own up to {max(segs)}: max-abs {err:.2e}",
           flush=True)
     assert err <= 2e-3
+
+
+def _prefix_shared_layer(seed, rows=64, prefix=256, n_q=32, n_kv=8, d=128, page=16):
+    """One prefix-shared attention layer: `rows` sequences share a
+    `prefix`-token node, each adds U[32, 256] own tokens; all pages are a
+    seeded permutation of the arena. The node's K/V are in the arena; the
+    rows' own K/V are chunk rows, scattered into their pages by the unified
+    path. Returns host tensors (the arena as rows, before the scatter)."""
+    g = torch.Generator().manual_seed(seed)
+    suf = torch.randint(32, 257, (rows,), generator=g)
+    own = [-(-int(n) // page) for n in suf]
+    n_pages = prefix // page + sum(own) + 8
+    perm = torch.randperm(n_pages, generator=g).to(torch.int32)
+    node_pages = perm[:prefix // page]
+    table = torch.zeros(rows, (prefix + 256) // page, dtype=torch.int32)
+    dst, at = [], prefix // page
+    for r, n in enumerate(suf.tolist()):
+        mine = perm[at:at + own[r]]
+        at += own[r]
+        table[r, :prefix // page] = node_pages
+        table[r, prefix // page:prefix // page + own[r]] = mine
+        j = torch.arange(n)
+        dst.append(mine[j // page].long() * page + j % page)
+    T = int(suf.sum())
+    sd = 1 / math.sqrt(d)
+    q = (torch.randn(T, n_q, d, generator=g) * sd).to(torch.bfloat16)
+    k3 = (torch.randn(T, n_kv, d, generator=g) * sd).to(torch.bfloat16)
+    v3 = (torch.randn(T, n_kv, d, generator=g) * sd).to(torch.bfloat16)
+    # arena rows no sequence reads hold NaN: nothing may read them
+    k_rows = torch.full((n_pages * page, n_kv, d), float("nan"), dtype=torch.bfloat16)
+    v_rows = torch.full((n_pages * page, n_kv, d), float("nan"), dtype=torch.bfloat16)
+    node_rows = node_pages[torch.arange(prefix) // page].long() * page + torch.arange(prefix) % page
+    k_rows[node_rows] = (torch.randn(prefix, n_kv, d, generator=g) * sd).to(torch.bfloat16)
+    v_rows[node_rows] = (torch.randn(prefix, n_kv, d, generator=g) * sd).to(torch.bfloat16)
+    cu = torch.zeros(rows + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(suf, 0)
+    return dict(q=q, k3=k3, v3=v3, k_rows=k_rows, v_rows=v_rows, table=table,
+                node_table=node_pages[None, :].contiguous(), dst=torch.cat(dst), cu=cu,
+                used=(prefix + suf).to(torch.int32), prefix=prefix, max_q=int(suf.max()),
+                n_kv=n_kv, scale=sd)
+
+
+def test_prefix_shared_layer_at_64_rows_every_path_matches_the_oracle():
+    """The attention layer the prefix-shared attention bench times (64 rows
+    x 256-token prefix, suffixes U[32, 256], 32/8 heads, permuted pages),
+    each path against the fp32 oracle on the GPU:
+      unified   scatter of the rows' K/V into their pages, then paged causal
+                attention over prefix + own pages (bf16 out and lse; its
+                fp8 epilogue is that output quantized, bit for bit);
+      tree      the fused kernel (node in full + own rows causal), bf16 out;
+      two_pass  call A (own rows, causal) and call B (node, stacked), each
+                against its oracle, and their merge against the oracle's
+                merge of the kernels' own outputs (scales within 1e-6
+                relative, at most 0.1 % of codes differing, by at most
+                an eighth of their group's largest value)."""
+    c = _prefix_shared_layer(61)
+    T, rows = int(c["cu"][-1]), c["cu"].numel() - 1
+    scale, n_kv = c["scale"], c["n_kv"]
+    kp = layout.k_pool_from_rows(c["k_rows"]).to(DEV)
+    vp = layout.v_pool_from_rows(c["v_rows"]).to(DEV)
+    qd, kd, vd, cu_d = c["q"].to(DEV), c["k3"].to(DEV), c["v3"].to(DEV), c["cu"].to(DEV)
+    node_tab, node_used = c["node_table"].to(DEV), torch.tensor([c["prefix"]],
+                                                                dtype=torch.int32, device=DEV)
+    seg_read = torch.zeros(rows, dtype=torch.int32, device=DEV)
+    with torch.no_grad():
+        want_tree = ref.tree_attention(qd, kd, vd, c["cu"], seg_read.cpu(), c["k_rows"].to(DEV),
+                                       c["v_rows"].to(DEV), c["node_table"],
+                                       torch.tensor([c["prefix"]], dtype=torch.int32), scale)
+    # tree: the fused kernel
+    got = K.tree_attention(qd, kd, vd, cu_d, seg_read, softmax_scale=scale, k_pool=kp,
+                           v_pool=vp, table=node_tab, used=node_used, fp8=False).float()
+    err_tree = (got - want_tree).abs().max().item()
+    # two-pass: call A over the rows' own K/V, call B over the node
+    a_len = (cu_d[1:] - cu_d[:-1]).to(torch.int32)
+    out_a, lse_a = K.attention(qd, cu_d, a_len, n_queries=T, max_q=c["max_q"],
+                               softmax_scale=scale, causal=True, k_rows=kd, v_rows=vd,
+                               cu_k=cu_d, n_kv=n_kv, want_lse=True)
+    cu_b = torch.tensor([0, T], dtype=torch.int32, device=DEV)
+    all_rows = torch.arange(T, dtype=torch.int64, device=DEV)
+    out_b, lse_b = K.attention(qd, cu_b, node_used, n_queries=T, max_q=T, softmax_scale=scale,
+                               causal=False, k_pool=kp, v_pool=vp, table=node_tab,
+                               q_rows=all_rows, n_kv=n_kv, want_lse=True)
+    with torch.no_grad():
+        want_a, want_la = ref.varlen_attention(qd, kd, vd, c["cu"], scale, causal=True)
+        want_b, want_lb = ref.paged_attention(qd, c["k_rows"].to(DEV), c["v_rows"].to(DEV),
+                                              torch.tensor([0, T], dtype=torch.int32),
+                                              torch.tensor([c["prefix"]], dtype=torch.int32),
+                                              c["node_table"], scale, False)
+    err_a = (out_a.float() - want_a).abs().max().item()
+    err_b = (out_b.float() - want_b).abs().max().item()
+    lse_ab = max((lse_a - want_la).abs().max().item(), (lse_b - want_lb).abs().max().item())
+    source = torch.arange(T, dtype=torch.int32, device=DEV)
+    q2, s2 = K.merge_attn_quant(out_a, lse_a, out_b, lse_b, source)
+    q2_ref, s2_ref = ref.merge_attn_quant(out_a.cpu(), lse_a.cpu(), out_b.cpu(), lse_b.cpu(),
+                                          source.cpu())
+    # unified: the rows' K/V into their own pages, then one paged call
+    K.kv_row_scatter(kd, vd, kp, vp, torch.arange(T, dtype=torch.int64, device=DEV),
+                     c["dst"].to(DEV))
+    k_after, v_after = c["k_rows"].clone(), c["v_rows"].clone()
+    k_after[c["dst"]], v_after[c["dst"]] = c["k3"], c["v3"]
+    args = dict(n_queries=T, max_q=c["max_q"], softmax_scale=scale, causal=True, k_pool=kp,
+                v_pool=vp, table=c["table"].to(DEV), n_kv=n_kv)
+    out_u, lse_u = K.attention(qd, cu_d, c["used"].to(DEV), want_lse=True, **args)
+    with torch.no_grad():
+        want_u, want_lu = ref.paged_attention(qd, k_after.to(DEV), v_after.to(DEV), c["cu"],
+                                              c["used"], c["table"], scale, True)
+    err_u = (out_u.float() - want_u).abs().max().item()
+    lse_u_err = (lse_u - want_lu).abs().max().item()
+    q8, s8 = K.attention_fp8(qd, cu_d, c["used"].to(DEV), **args)
+    rq, rs = K.group_quant(out_u.view(T, -1))
+    # unified and tree compute one function: the oracles agree
+    oracles = (want_u - want_tree).abs().max().item()
+    print(f"prefix-shared layer, {rows} rows / {T} query rows: unified {err_u:.2e} "
+          f"(lse {lse_u_err:.2e}), tree {err_tree:.2e}, call A {err_a:.2e}, call B "
+          f"{err_b:.2e} (lse {lse_ab:.2e}); oracles apart {oracles:.2e}", flush=True)
+    assert oracles <= 1e-5
+    assert err_u <= 2e-3 and lse_u_err <= 2e-3
+    assert torch.equal(q8.view(torch.uint8), rq.view(torch.uint8)) and torch.equal(s8, rs)
+    assert err_tree <= 2e-3
+    assert err_a <= 2e-3 and err_b <= 2e-3 and lse_ab <= 2e-3
+    # the merge kernel's weight (hardware exp) and its fused a + (b - a) w may
+    # round a bf16 step apart from torch's; where a and b nearly cancel that
+    # moves a small value's e4m3 code by several steps of its own scale, so
+    # the bar is one step at the top of the group: |dequantized difference|
+    # <= amax / 8 per (row, head) group, and differing codes rare
+    assert torch.allclose(s2.cpu(), s2_ref, rtol=1e-6, atol=0)
+    s2c = s2.cpu()
+    steps = _e4m3_steps(q2.cpu(), q2_ref)
+    deq = q2.cpu().float().view(T, -1, 128) * s2c[:, :, None]
+    deq_ref = q2_ref.float().view(T, -1, 128) * s2_ref[:, :, None]
+    top = ((deq - deq_ref).abs().amax(-1) / (448 * s2_ref)).max().item()
+    frac = (steps > 0).float().mean().item()
+    print(f"two-pass merge + quant against the oracle's merge of the same outputs: "
+          f"{frac:.2e} of codes differ, at most {steps.max().item()} steps, largest "
+          f"difference {top:.3f} of the group's amax", flush=True)
+    assert frac <= 1e-3 and top <= 0.125
 
 
 # ---------------------------------------------------------------------------

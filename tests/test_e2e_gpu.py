@@ -19,8 +19,9 @@ output). The bars, written in the tests:
   - decisions, against the noise of the two oracle forms measured in the
     same test: every row whose margin lies beyond twice the 99th
     percentile of the oracles' margin shift is decided as the oracle
-    decides it, the GPU's margins move at most twice as far, and it
-    disagrees on at most about twice as many rows as the oracles do.
+    decides it, the GPU's median margin shift is at most 2.5 times the
+    oracle pair's, and it disagrees on at most about twice as many rows as
+    the oracles do.
 """
 
 from dataclasses import replace
@@ -453,12 +454,13 @@ def test_qwen3_4b_decisions_agree_with_the_oracle_within_its_noise():
 
     They are not well posed: 36 layers of dynamic 1x128 fp8 re-quantization
     amplify a one-ulp difference until the two oracles disagree on about
-    one row in eight, with margin shifts as large as the median margin
+    one row in ten, with margin shifts as large as the median margin
     (scaling the layers' residual writes down by 10x does not change
-    that). So the bars are that every row the GPU decides differently
-    from the fp64 oracle lies inside twice the oracles' largest margin
-    shift, and that the GPU agrees with it as often as the other oracle
-    does, within three binomial standard deviations of the two counts."""
+    that). The band is the 99th percentile of the oracle pair's margin
+    shift. Bars: every row whose fp64 margin lies beyond twice the band is
+    decided as the fp64 oracle decides it, and the GPU agrees with that
+    oracle as often as the other oracle does, within three binomial
+    standard deviations of the two counts."""
     from quail_amd.aiif import synthetic_filter_workload
     from quail_amd.model import SYNTHETIC_FALSE_IDS, SYNTHETIC_TRUE_IDS
     from quail_amd.specs import QWEN3_4B_FP8
@@ -491,20 +493,11 @@ def test_qwen3_4b_decisions_agree_with_the_oracle_within_its_noise():
         runs[name] = (bits, marg)
         del arena
         torch.cuda.empty_cache()
-    (ref_bits, ref_m), (alt_bits, alt_m) = runs["fp64"], runs["fp32"]
-    shift = max(abs(ref_m[d] - alt_m[d]) for d in range(n))
-    band = 2 * shift
-    floor = sum(ref_bits[d] == alt_bits[d] for d in range(n))
-    agree = sum(answers[d] == ref_bits[d] for d in range(n))
-    gpu_shift = max(abs(margins[d] - ref_m[d]) for d in range(n))
-    typical = float(np.median([abs(ref_m[d]) for d in range(n)]))
-    print(f"GPU-vs-oracle {agree}/{n}, oracle-vs-oracle {floor}/{n}; largest margin shift "
-          f"oracle-vs-oracle {shift:.4f}, GPU-vs-oracle {gpu_shift:.4f}; median |margin| "
-          f"{typical:.4f}", flush=True)
-    for d in range(n):
-        if answers[d] != ref_bits[d]:
-            assert abs(ref_m[d]) <= band, \
-                f"row {d}: decision differs at margin {ref_m[d]:.4f} (noise band {band:.4f})"
+    stats = decision_stats((answers, margins), runs["fp64"], runs["fp32"])
+    print(f"{describe(stats)}; oracle margins of the rows decided differently "
+          f"{stats['disagree_margins']}", flush=True)
+    assert stats["gpu_agree_wide"] == stats["outside_wide"], stats
+    floor, agree = stats["floor"], stats["gpu_agree"]
     q = 1.0 - floor / n
     slack = 3.0 * (2.0 * n * q * (1.0 - q)) ** 0.5
     assert agree >= floor - slack, f"GPU agrees on {agree}/{n}, the oracles on {floor}/{n}"
