@@ -925,6 +925,10 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
   const int own_keys = min(count, i0 + BQ);            // causal: rows < i0 + 32
   const int n_tiles = n1 + (own_keys + BKV - 1) / BKV;
   const int my_i = i0 + col;
+  // what the epilogue needs, pinned to VGPRs: held as scalars across the
+  // tile loops they were spilled to VGPR lanes and read back by v_readlane
+  int ep_row0 = q0 + i0, ep_rows = count - i0, ep_hq = hq, ep_stage = wave * 32 * 144;
+  asm volatile("" : "+v"(ep_row0), "+v"(ep_rows), "+v"(ep_hq), "+v"(ep_stage));
 
   // ---- DMA roles: wave (region, pit) moves K (region 0) or V (region 1) of
   // keys 16 pit .. 16 pit + 15 of a tile, as four 1 KiB pieces -------------
@@ -1221,7 +1225,7 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
   // ---- epilogue -------------------------------------------------------------
   const float l_tot = xor32_sum(l_run);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  const long qi = q0 + my_i;
+  const long qi = (long)ep_row0 + col;
   if constexpr (FP8OUT) {
     float amax = 0.f;
 #pragma unroll
@@ -1250,15 +1254,15 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
     // every wave is past its last read of the stages (and every DMA landed)
     // before the stages become staging rows
     wg_barrier();
-    store_fp8_rows(lds + wave * 32 * 144, w, lane,
-                   E->out_q + (long)(q0 + i0) * E->ld_out_q + (long)hq * D, E->ld_out_q,
-                   count - i0);
-    if (my_i >= count) return;
-    if (half == 0) E->out_scales[(long)hq * E->n_rows + qi] = scale;
+    store_fp8_rows(lds + ep_stage, w, lane,
+                   E->out_q + (long)ep_row0 * E->ld_out_q + (long)ep_hq * D, E->ld_out_q,
+                   ep_rows);
+    if (col >= ep_rows) return;
+    if (half == 0) E->out_scales[(long)ep_hq * E->n_rows + qi] = scale;
   } else {
-    if (my_i >= count) return;
+    if (col >= ep_rows) return;
     const auto* E = late_params<TreeParams>();
-    uint16_t* op = E->out + qi * E->ldo + (long)hq * D;
+    uint16_t* op = E->out + qi * E->ldo + (long)ep_hq * D;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
