@@ -290,6 +290,10 @@ def main():
                          "file (the reference's scan input) or from in-memory arrays")
     ap.add_argument("--attention", default=None, choices=["unified", "tree"],
                     help="default: unified for filters, tree for the join")
+    ap.add_argument("--tree-kernel", default="fused", choices=["fused", "resident", "two_pass"],
+                    help="the tree path's attention kernel (aiif and join workloads): node "
+                         "pages streamed per q-tile, a node's K/V held in LDS, or the "
+                         "three-launch form")
     ap.add_argument("--arena-pages", type=int, default=None)
     ap.add_argument("--cpu-rows", type=int, default=8)
     ap.add_argument("--ue8m0", action="store_true",
@@ -359,7 +363,8 @@ def main():
     clock.n_q, clock.d, clock.n_kv = spec.n_q, spec.d_head, spec.n_kv
     runner = FilterRunner(model, spec, device_spec=MI355X, n_pages=args.arena_pages,
                           attention_mode=args.attention, gemm_hook=clock.gemm_hook,
-                          attention_hook=clock.attention_hook, ue8m0=args.ue8m0)
+                          attention_hook=clock.attention_hook, ue8m0=args.ue8m0,
+                          tree_kernel=args.tree_kernel)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t_build
 
@@ -433,6 +438,7 @@ def main():
                        + (", UE8M0 scales applied by the MFMA" if args.ue8m0
                           else ", fp32 block scales")),
                    "rows": args.rows, "layers": spec.layers,
+                   "tree_kernel": args.tree_kernel if args.attention == "tree" else None,
                    "fresh_tokens": stats["fresh_tokens"],
                    "input_tokens": stats["input_tokens"], "chunks": stats.get("chunks"),
                    "chunk_budget": runner.budget, "arena_pages": runner.arena.n_pages},
@@ -761,7 +767,7 @@ def join_bench(args):
     clock.n_q, clock.d, clock.n_kv = spec.n_q, spec.d_head, spec.n_kv
     runner = JoinRunner(model, spec, device_spec=MI355X, n_pages=args.arena_pages,
                         attention_mode=attention, gemm_hook=clock.gemm_hook,
-                        attention_hook=clock.attention_hook)
+                        attention_hook=clock.attention_hook, tree_kernel=args.tree_kernel)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t_build
     for _ in range(args.warmup):
@@ -811,6 +817,7 @@ def join_bench(args):
                                 f"median 120, cap 512) + 16-token tail, {attention} "
                                 f"attention"),
                    "pairs": pairs, "anchors": args.anchors, "partners": args.partners,
+                   "tree_kernel": args.tree_kernel if attention == "tree" else None,
                    "layers": spec.layers, "fresh_tokens": stats["fresh_tokens"],
                    "input_tokens": stats["input_tokens"], "chunks": stats.get("chunks"),
                    "borrowed_tokens": stats.get("borrowed_tokens"),

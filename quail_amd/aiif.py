@@ -81,11 +81,15 @@ class FilterRunner:
         budget: chunk tokens; None uses budgets.chunk_budget.
         attention_mode: "unified", "tree" or None (unified).
         gemm_hook: passed to the engine (GEMM timing in bench.py).
+        tree_kernel: the tree path's attention kernel, "fused" (node pages
+            streamed per q-tile), "resident" (a node's K/V held in LDS for
+            the q-tiles that read it) or "two_pass" (the reference's three
+            launches).
     """
 
     def __init__(self, model, spec, *, device_spec=MI355X, n_pages=None, budget=None,
                  attention_mode=None, ue8m0=False, gemm_hook=None, attention_hook=None,
-                 keep_margins=True,
+                 keep_margins=True, tree_kernel="fused",
                  true_ids=SYNTHETIC_TRUE_IDS, false_ids=SYNTHETIC_FALSE_IDS):
         import torch
         self.torch = torch
@@ -97,7 +101,8 @@ class FilterRunner:
         self.arena = KVArena(n_layers, n_pages, budgets.PAGE_TOKENS, spec.n_kv,
                              spec.d_head, dtype=torch.bfloat16, device="cuda")
         self.pipeline = Qwen3Pipeline(model, self.arena, spec=spec, ue8m0=ue8m0,
-                                      gemm_hook=gemm_hook, attention_hook=attention_hook)
+                                      gemm_hook=gemm_hook, attention_hook=attention_hook,
+                                      tree_kernel=tree_kernel)
         self.rows = AnswerRows(torch, model, true_ids, false_ids)
         self.answers = AsyncAnswers(torch, self.rows, keep_margins=keep_margins)
         self.attention_mode = attention_mode
