@@ -444,9 +444,11 @@ def test_join_decisions_agree_outside_the_noise_band(path):
     print(f"join {path}: GPU-vs-oracle {agree}/{total} final rows")
 
 
-def test_qwen3_4b_decisions_agree_with_the_oracle_within_its_noise():
+@pytest.mark.parametrize("path", ["unified", "tree"])
+def test_qwen3_4b_decisions_agree_with_the_oracle_within_its_noise(path):
     """Full Qwen3-4B geometry (36 layers, random init) over the first 192
-    rows of the seeded 4096-row filter workload, unified path, four chunks.
+    rows of the seeded 4096-row filter workload, four chunks, on each
+    attention path (the oracle replays the chunks on the path they ran).
     The oracle replays every chunk on the GPU (the same torch functions the
     CPU runs, on device tensors) twice: with fp64 block sums and with
     dequantize-then-fp32 GEMMs. The two are equally valid restatements, so
@@ -472,11 +474,11 @@ def test_qwen3_4b_decisions_agree_with_the_oracle_within_its_noise():
     docs = [np.concatenate([instruction, d]) for d in documents[:n]]
     pages = sum(-(-(len(d) + len(tail)) // 16) for d in docs) + 64
     answers, margins, records, stream = gpu_filter(
-        model, spec, docs, tail, path="unified", pages=pages, budget=16384,
+        model, spec, docs, tail, path=path, pages=pages, budget=16384,
         true_ids=SYNTHETIC_TRUE_IDS, false_ids=SYNTHETIC_FALSE_IDS)
-    assert len(records) >= 3
-    print(f"{len(records)} chunks, {sum(len(r[0]['positions']) for r in records)} tokens",
-          flush=True)
+    assert len(records) >= 3 and all(mode == path for _, mode, _ in records)
+    print(f"{path}: {len(records)} chunks, "
+          f"{sum(len(r[0]['positions']) for r in records)} tokens", flush=True)
 
     torch.backends.cuda.matmul.allow_tf32 = False
     w = oforward.oracle_weights(model, "cuda")
