@@ -300,6 +300,8 @@ def main():
                     help="power-of-two (UE8M0) activation and weight scales, applied by the "
                          "MFMA: the reference's DeepGEMM UE8M0 mode (aiif-4b, gemm-c2)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--progress", action="store_true",
+                    help="aiif workloads: a line on stderr after each chunk's answers")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (fp32 x * 1) three times: "
@@ -368,15 +370,26 @@ def main():
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t_build
 
+    done = None
+    if args.progress:
+        # a line on stderr per chunk report: rows answered so far in this pass
+        count = [0]
+
+        def done(finished):
+            count[0] += len(finished)
+            print(f"[{time.perf_counter() - t_build:8.1f}s] {count[0] % args.rows or args.rows}"
+                  f"/{args.rows} rows answered", file=sys.stderr, flush=True)
+
     for _ in range(args.warmup):
-        runner.run(instruction, documents, tail)
+        runner.run(instruction, documents, tail, document_done=done)
     clock.active = True
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     results = []
     host = {}   # host-side phases of the loop (admission, allocation, packing, ...)
     for _ in range(args.steps):
-        answers, stats = runner.run(instruction, documents, tail, timing=host)
+        answers, stats = runner.run(instruction, documents, tail, timing=host,
+                                    document_done=done)
         results.append((answers, stats))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0

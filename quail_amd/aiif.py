@@ -108,8 +108,10 @@ class FilterRunner:
         self.attention_mode = attention_mode
         self.last = {}
 
-    def run(self, instruction, documents, tail, *, timing=None):
-        """Run the filter; returns (answers per row, stats)."""
+    def run(self, instruction, documents, tail, *, timing=None, document_done=None):
+        """Run the filter; returns (answers per row, stats). document_done,
+        if given, is called after each chunk's report with the documents it
+        finished, as [(doc, stage, passed)]."""
         torch = self.torch
         docs = RowPrompts(instruction, documents)
         tree = prefix_tree(docs, budgets.PAGE_TOKENS)
@@ -120,7 +122,8 @@ class FilterRunner:
         answers, _, tokens = loop.run_filter(
             torch, self.arena, self.pipeline, self.answers, docs, [list(tail)],
             self.budget, timing=timing, arena_writes=True,
-            attention_mode=self.attention_mode, prefix_tree=tree, stats=stats)
+            attention_mode=self.attention_mode, prefix_tree=tree, stats=stats,
+            document_done=document_done)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         if self.arena.accounting.owned:
