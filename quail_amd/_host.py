@@ -19,7 +19,10 @@ import threading
 import numpy as np
 
 LIB_NAME = "libquail_host.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# QUAIL_HOST_LIB names another build of the same sources, e.g. the
+# AddressSanitizer one (`make -C quail_amd/host asan`)
+LIB_PATH = os.environ.get("QUAIL_HOST_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 QP_OK, QP_NONE = 0, 1
 QP_E_KEY, QP_E_VALUE, QP_E_STATE, QP_E_ARENA_FULL = -1, -2, -3, -4
