@@ -1861,7 +1861,8 @@ extern "C" int qh_attention_fp8(const void* q, long ldq, int q_rows_total,
                                 float softmax_scale, int causal, void* out_q, long ld_out_q,
                                 float* scales, int ue8m0, void* workspace,
                                 size_t workspace_bytes, qh_stream_t stream) {
-  QH_REQUIRE(table && out_q && scales, "attention_fp8: paged call needs table, out_q, scales");
+  QH_REQUIRE(n_seqs == 0 || n_queries == 0 || (table && out_q && scales),
+             "attention_fp8: paged call needs table, out_q, scales");
   return attention_launch(q, ldq, q_rows_total, q_rows, k_pool, v_pool, pool_pages, table,
                           table_width, page_tokens, nullptr, nullptr, 0, nullptr, cu_q, kv_len,
                           n_seqs, n_queries, max_q, n_q, n_kv, d, softmax_scale, causal,

@@ -551,7 +551,6 @@ extern "C" int qh_add_rmsnorm_quant(const void* x, long ldx, void* residual,
                                     long ld_res, const void* w, float eps,
                                     int T, int H, void* out_q, float* scales,
                                     int ue8m0, qh_stream_t stream) {
-  QH_REQUIRE(x && w && out_q && scales, "add_rmsnorm_quant: null pointer");
   QH_REQUIRE(T >= 0, "add_rmsnorm_quant: T=%d", T);
   QH_REQUIRE(H > 0 && H % 512 == 0 && H <= 8192,
              "add_rmsnorm_quant: H=%d must be a positive multiple of 512 up to 8192", H);
@@ -559,6 +558,7 @@ extern "C" int qh_add_rmsnorm_quant(const void* x, long ldx, void* residual,
   QH_REQUIRE(ldx % 8 == 0 && (!residual || ld_res % 8 == 0),
              "add_rmsnorm_quant: row strides must be multiples of 8");
   if (T == 0) return QH_OK;
+  QH_REQUIRE(x && w && out_q && scales, "add_rmsnorm_quant: null pointer");
   dim3 grid(blocks_for(T, 4)), block(256);
   const int vpl = H / 512;
   auto args = [&](auto kern) {
@@ -574,10 +574,10 @@ extern "C" int qh_add_rmsnorm_quant(const void* x, long ldx, void* residual,
 
 extern "C" int qh_group_quant(const void* x, long ldx, int T, int W, void* out_q,
                               float* scales, int ue8m0, qh_stream_t stream) {
-  QH_REQUIRE(x && out_q && scales, "group_quant: null pointer");
   QH_REQUIRE(T >= 0 && W > 0 && W % 128 == 0, "group_quant: W=%d must be a multiple of 128", W);
   QH_REQUIRE(ldx >= W && ldx % 8 == 0, "group_quant: row stride %ld", ldx);
   if (T == 0) return QH_OK;
+  QH_REQUIRE(x && out_q && scales, "group_quant: null pointer");
   const long groups = (long)T * (W / 128);
   hipLaunchKernelGGL(group_quant_kernel, dim3(blocks_for(groups, 16)), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)x, ldx, T, W,
@@ -588,10 +588,10 @@ extern "C" int qh_group_quant(const void* x, long ldx, int T, int W, void* out_q
 extern "C" int qh_silu_mul_quant(const void* gate_up, long ld, int T, int I,
                                  void* out_q, float* scales, int ue8m0,
                                  qh_stream_t stream) {
-  QH_REQUIRE(gate_up && out_q && scales, "silu_mul_quant: null pointer");
   QH_REQUIRE(T >= 0 && I > 0 && I % 128 == 0, "silu_mul_quant: I=%d must be a multiple of 128", I);
   QH_REQUIRE(ld >= 2L * I && ld % 8 == 0, "silu_mul_quant: row stride %ld", ld);
   if (T == 0) return QH_OK;
+  QH_REQUIRE(gate_up && out_q && scales, "silu_mul_quant: null pointer");
   const long groups = (long)T * (I / 128);
   hipLaunchKernelGGL(silu_mul_quant_kernel, dim3(blocks_for(groups, 16)), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)gate_up, ld, T, I,
@@ -604,13 +604,13 @@ extern "C" int qh_qk_norm_rope(const void* qkv, long ld_qkv, const int64_t* posi
                                const void* kw, float eps, int T, int n_q, int n_kv,
                                int d, void* q_out, void* k_out, void* v_out,
                                qh_stream_t stream) {
-  QH_REQUIRE(qkv && positions && cos_sin && qw && kw && q_out && k_out && v_out,
-             "qk_norm_rope: null pointer");
   QH_REQUIRE(d == 128, "qk_norm_rope: head_dim %d unsupported (128 only)", d);
   QH_REQUIRE(n_q > 0 && n_kv > 0 && T >= 0 && max_pos > 0, "qk_norm_rope: geometry");
   QH_REQUIRE(ld_qkv >= (long)(n_q + 2 * n_kv) * d && ld_qkv % 8 == 0,
              "qk_norm_rope: row stride %ld", ld_qkv);
   if (T == 0) return QH_OK;
+  QH_REQUIRE(qkv && positions && cos_sin && qw && kw && q_out && k_out && v_out,
+             "qk_norm_rope: null pointer");
   dim3 grid(T, blocks_for(n_q + 2 * n_kv, 16));
   hipLaunchKernelGGL(qk_norm_rope_kernel, grid, dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)qkv, ld_qkv, positions, (const uint16_t*)cos_sin,
@@ -679,9 +679,9 @@ extern "C" int qh_merge_attn_quant(const void* out_a, const float* lse_a,
                                    const float* lse_b, long lse_b_stride,
                                    const int32_t* source, int T, int n_h, void* out_q,
                                    float* scales, int ue8m0, qh_stream_t stream) {
-  QH_REQUIRE(out_a && lse_a && source && out_q && scales, "merge_attn_quant: null pointer");
   QH_REQUIRE(T >= 0 && n_h > 0, "merge_attn_quant: geometry");
   if (T == 0) return QH_OK;
+  QH_REQUIRE(out_a && lse_a && source && out_q && scales, "merge_attn_quant: null pointer");
   QH_REQUIRE(out_b && lse_b, "merge_attn_quant: out_b/lse_b null");
   const long groups = (long)T * n_h;
   hipLaunchKernelGGL(merge_attn_quant_kernel, dim3(blocks_for(groups, 16)), dim3(256), 0,

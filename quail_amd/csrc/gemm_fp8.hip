@@ -843,8 +843,8 @@ static int gemm_qkv_rope(const void* A, long lda, const float* sa, const void* B
                          const int64_t* positions, const void* cos_sin, int max_pos,
                          const void* q_w, const void* k_w, float eps, void* q_out, long ld_q,
                          void* k_out, void* v_out, long ld_kv, void* k_pool, void* v_pool,
-                         const int64_t* row_dst, int page_tokens, bool hw, qh_stream_t stream,
-                         const char* what) {
+                         const int64_t* row_dst, int page_tokens, bool arena, bool hw,
+                         qh_stream_t stream, const char* what) {
   QH_REQUIRE(M >= 0 && K > 0 && n_q > 0 && n_kv > 0, "%s: M=%d K=%d n_q=%d n_kv=%d", what, M,
              K, n_q, n_kv);
   QH_REQUIRE(n_q % 2 == 0 && n_kv % 2 == 0 && n_q % n_kv == 0,
@@ -856,7 +856,6 @@ static int gemm_qkv_rope(const void* A, long lda, const float* sa, const void* B
              "%s: lda/ldb must be >= K and multiples of 16 bytes", what);
   QH_REQUIRE(ld_q >= n_q * 128 && ld_q % 8 == 0, "%s: ld_q=%ld", what, ld_q);
   QH_REQUIRE(offsets_fit(M, N, K, lda, ldb), "%s: operands exceed 2 GiB offsets", what);
-  const bool arena = row_dst != nullptr;
   if (arena) {
     QH_REQUIRE(page_tokens == 16, "%s: page_tokens=%d (the arena's pages hold 16 tokens)", what,
                page_tokens);
@@ -885,7 +884,7 @@ extern "C" int qh_fp8_gemm_qkv_rope(const void* A, long lda, const float* sa, co
                                     long ld_kv, int ue8m0_scales, qh_stream_t stream) {
   return gemm_qkv_rope(A, lda, sa, B, ldb, sb, M, K, n_q, n_kv, positions, cos_sin, max_pos,
                        q_w, k_w, eps, q_out, ld_q, k_out, v_out, ld_kv, nullptr, nullptr,
-                       nullptr, 16, ue8m0_scales != 0, stream, "fp8_gemm_qkv_rope");
+                       nullptr, 16, false, ue8m0_scales != 0, stream, "fp8_gemm_qkv_rope");
 }
 
 extern "C" int qh_fp8_gemm_qkv_rope_kv(const void* A, long lda, const float* sa,
@@ -899,7 +898,7 @@ extern "C" int qh_fp8_gemm_qkv_rope_kv(const void* A, long lda, const float* sa,
   QH_REQUIRE(row_dst != nullptr || M == 0, "fp8_gemm_qkv_rope_kv: row_dst is null");
   return gemm_qkv_rope(A, lda, sa, B, ldb, sb, M, K, n_q, n_kv, positions, cos_sin, max_pos,
                        q_w, k_w, eps, q_out, ld_q, nullptr, nullptr, 0, k_pool, v_pool, row_dst,
-                       page_tokens, ue8m0_scales != 0, stream, "fp8_gemm_qkv_rope_kv");
+                       page_tokens, true, ue8m0_scales != 0, stream, "fp8_gemm_qkv_rope_kv");
 }
 
 extern "C" int qh_fp8_gemm_nt(const void* A, long lda, const float* sa, const void* B,

@@ -81,7 +81,7 @@ def _check_gemm(a, a_scales, w, w_scales):
     if w.shape[1] != K:
         raise ValueError(f"K mismatch: a {tuple(a.shape)} w {tuple(w.shape)}")
     if a_scales.dtype != torch.float32 or tuple(a_scales.shape) != (M, K // GROUP) \
-            or (M > 1 and a_scales.stride(0) != 1) or a_scales.stride(1) != M:
+            or (M > 1 and a_scales.stride(0) != 1) or (M > 0 and a_scales.stride(1) != M):
         raise ValueError("a_scales must be a (M, K/128) view of column-major fp32")
     if w_scales.dtype != torch.float32 or tuple(w_scales.shape) != (N // GROUP, K // GROUP) \
             or not w_scales.is_contiguous():

@@ -897,3 +897,93 @@ def test_tree_attention_agrees_with_the_two_pass_form():
                        torch.full_like(mag, 2.0 ** -9)) * scale
     beyond = ((two - one).abs() > step * 1.001).float().mean().item()
     assert beyond < 0.05, f"values off by more than one e4m3 step: {beyond}"
+
+
+def test_every_entry_point_takes_empty_inputs():
+    """Zero rows (an empty chunk, no answer rows, no reads) through every
+    entry point: each returns empty outputs of the right shapes and launches
+    nothing; the sizes check before the pointers, since an empty tensor's
+    storage may be null."""
+    bf, f8 = torch.bfloat16, torch.float8_e4m3fn
+    H, n_q, n_kv, d = 2560, 32, 8, 128
+    e_bf = torch.empty(0, H, dtype=bf, device=DEV)
+    w = torch.ones(H, dtype=bf, device=DEV)
+    q, s = K.add_rmsnorm_quant(e_bf, w, 1e-6)
+    assert q.shape == (0, H) and s.shape == (0, H // 128)
+    q, s = K.add_rmsnorm_quant(e_bf, w, 1e-6, residual=torch.empty(0, H, dtype=bf, device=DEV))
+    assert q.shape == (0, H)
+    q, s = K.group_quant(e_bf)
+    assert q.shape == (0, H) and s.shape == (0, H // 128)
+    q, s = K.silu_mul_quant(torch.empty(0, 2 * H, dtype=bf, device=DEV))
+    assert q.shape == (0, H)
+    # GEMMs with no rows
+    a = torch.empty(0, H, dtype=f8, device=DEV)
+    a_s = K.col_major_scales(0, H, DEV)
+    wq = torch.zeros(512, H, dtype=f8, device=DEV)
+    ws = torch.ones(4, H // 128, dtype=torch.float32, device=DEV)
+    assert K.fp8_gemm_nt(a, a_s, wq, ws).shape == (0, 512)
+    q, s = K.fp8_gemm_silu_quant(a, a_s, wq, ws)
+    assert q.shape == (0, 256) and s.shape == (0, 2)
+    wqkv = torch.zeros((n_q + 2 * n_kv) * d, H, dtype=f8, device=DEV)
+    wqkv_s = torch.ones((n_q + 2 * n_kv), H // 128, dtype=torch.float32, device=DEV)
+    cos_sin = torch.zeros(64, d, dtype=bf, device=DEV)
+    hw = torch.ones(d, dtype=bf, device=DEV)
+    pos = torch.empty(0, dtype=torch.int64, device=DEV)
+    qq, kk, vv = K.fp8_gemm_qkv_rope(a, a_s, wqkv, wqkv_s, pos, cos_sin, hw, hw, 1e-6, n_q, n_kv)
+    assert qq.shape == (0, n_q * d) and kk.shape == vv.shape == (0, n_kv * d)
+    kp = torch.zeros(4, n_kv, 16, d, dtype=bf, device=DEV)
+    vp = torch.zeros(4, n_kv, d, 16, dtype=bf, device=DEV)
+    qq = K.fp8_gemm_qkv_rope(a, a_s, wqkv, wqkv_s, pos, cos_sin, hw, hw, 1e-6, n_q, n_kv,
+                             k_pool=kp, v_pool=vp, row_dst=pos)
+    assert qq.shape == (0, n_q * d) and not kp.any() and not vp.any()
+    qkv = torch.empty(0, (n_q + 2 * n_kv) * d, dtype=bf, device=DEV)
+    qq, kk, vv = K.qk_norm_rope(qkv, pos, cos_sin, hw, hw, 1e-6, n_q, n_kv, d)
+    assert qq.shape == (0, n_q * d)
+    assert K.qk_norm_rope_kv(qkv, pos, cos_sin, hw, hw, 1e-6, n_q, n_kv, d, kp, vp,
+                             pos).shape == (0, n_q * d)
+    # KV movement with nothing to move
+    rows = torch.empty(0, n_kv, d, dtype=bf, device=DEV)
+    K.kv_row_scatter(rows, rows, kp, vp, pos, pos)
+    K.kv_row_copy(kp, vp, pos, pos)
+    assert not kp.any() and not vp.any()
+    # attention over no sequences, and over sequences with no query rows
+    q3 = torch.empty(0, n_q, d, dtype=bf, device=DEV)
+    table = torch.zeros(2, 4, dtype=torch.int32, device=DEV)
+    used = torch.tensor([16, 32], dtype=torch.int32, device=DEV)
+    for cu in (torch.zeros(1, dtype=torch.int32, device=DEV),
+               torch.zeros(3, dtype=torch.int32, device=DEV)):
+        n_seqs = cu.numel() - 1
+        out, lse = K.attention(q3, cu, used[:n_seqs], n_queries=0, max_q=0, softmax_scale=0.1,
+                               causal=True, k_pool=kp, v_pool=vp, table=table[:max(n_seqs, 1)],
+                               n_kv=n_kv, want_lse=True)
+        assert out.shape == (0, n_q, d) and lse.shape == (n_q, 0)
+        q8, s8 = K.attention_fp8(q3, cu, used[:n_seqs], n_queries=0, max_q=0,
+                                 softmax_scale=0.1, causal=True, k_pool=kp, v_pool=vp,
+                                 table=table[:max(n_seqs, 1)], n_kv=n_kv)
+        assert q8.shape == (0, n_q * d) and s8.shape == (0, n_q)
+    for resident in (False, True):
+        q8, s8 = K.tree_attention(q3, rows, rows, torch.zeros(1, dtype=torch.int32, device=DEV),
+                                  torch.empty(0, dtype=torch.int32, device=DEV),
+                                  softmax_scale=0.1, k_pool=kp, v_pool=vp, table=table,
+                                  used=used, resident=resident)
+        assert q8.shape == (0, n_q * d) and s8.shape == (0, n_q)
+    lse0 = torch.empty(n_q, 0, dtype=torch.float32, device=DEV)
+    q8, s8 = K.merge_attn_quant(q3, lse0, q3, lse0, torch.empty(0, dtype=torch.int32,
+                                                                device=DEV))
+    assert q8.shape == (0, n_q * d)
+    # row gathers, norms and the readout with no rows
+    idx = torch.empty(0, dtype=torch.int64, device=DEV)
+    table_rows = torch.ones(10, H, dtype=bf, device=DEV)
+    assert K.gather_rows(table_rows, idx).shape == (0, H)
+    full = torch.ones(5, H, dtype=bf, device=DEV)
+    assert K.final_norm(full, full.clone(), idx, w, 1e-6).shape == (0, H)
+    hid, res = K.fused_add_rms_norm(e_bf.clone(), e_bf.clone(), w, 1e-6)
+    assert hid.shape == res.shape == (0, H)
+    w_ans = torch.ones(4, H, dtype=bf, device=DEV)
+    is_true = torch.tensor([1, 1, 0, 0], dtype=torch.uint8, device=DEV)
+    bits, margin = K.answer_bits(e_bf, w_ans, is_true)
+    assert bits.shape == margin.shape == (0,)
+    t, f = K.answer_logits(e_bf, w_ans, is_true)
+    assert t.shape == f.shape == (0,)
+    assert K.e4m3_encode(torch.empty(0, dtype=torch.float32, device=DEV)).shape == (0,)
+    torch.cuda.synchronize()
