@@ -54,6 +54,35 @@ def test_argument_errors_raise_value_error_without_a_gpu():
                   None, 0, None, 0, None, 0, None)
 
 
+# (entry point, arguments, the error message's words): geometry the kernels
+# cannot take, rejected before any pointer is read or HIP call made
+REJECTED = [
+    # a weight whose int32 element offsets would pass 2^31 (1,048,576 rows x 2,560)
+    ("qh_fp8_gemm_nt", (None, 2560, None, None, 2560, None, None, 1 << 20, 16, 1 << 20, 2560,
+                        None), "exceed 2 GiB"),
+    ("qh_fp8_gemm_silu_quant", (None, 2560, None, None, 2560, None, 16, 1 << 19, 2560, None,
+                                1 << 19, None, 0, None), "exceed 2 GiB"),
+    ("qh_fp8_gemm_nt", (None, 2560, None, None, 2560, None, None, 19456, 16, 19456, 2500, None),
+     "multiple of 128"),
+    ("qh_group_quant", (None, 128, 4, 100, None, None, 0, None), "multiple of 128"),
+    ("qh_e4m3_encode", (None, 6, None, None), "multiple of 4"),
+    # more sequences than the no-allocation entry's static scratch holds
+    ("qh_attention_fp8_noalloc", (None, 4096, 1, None, None, None, 1, None, 1, 16, None, None,
+                                  10_000_000, 1, 1, 32, 8, 128, 0.1, 1, None, 4096, None, 0,
+                                  None), "static scratch holds at most"),
+    # a GQA group the tree kernel's head groups cannot tile (6 / 4 heads)
+    ("qh_tree_attention", (None, 768, 1, None, None, 512, None, None, 1, None, None, 0, None, 0,
+                           None, 0, 16, 6, 4, 128, 0.1, None, 0, None, 0, None, 0, None, 0,
+                           None), "GQA group"),
+]
+
+
+@pytest.mark.parametrize("name,args,words", REJECTED, ids=[f"{r[0]}-{r[2]}" for r in REJECTED])
+def test_unsupported_geometry_is_rejected_before_any_launch(name, args, words):
+    with pytest.raises(ValueError, match=words):
+        _hip.call(name, *args)
+
+
 HOST_HEADER = os.path.join(ROOT, "include", "quail_host.h")
 
 
