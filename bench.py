@@ -311,7 +311,7 @@ def main():
         copy_calibration(args.copy_calibration)
         return
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for {args.gpus}): this build has no "
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}): quail_amd has no "
               f"multi-GPU path; rows shard per GPU with no device communication.",
               file=sys.stderr)
         sys.exit(2)

@@ -43,7 +43,7 @@ typedef struct ihipStream_t* qh_stream_t;
 enum {
   QH_OK = 0,
   QH_E_ARGUMENT = -1,     /* bad pointer, size or geometry   -> ValueError   */
-  QH_E_UNSUPPORTED = -2,  /* geometry this build has no kernel for          */
+  QH_E_UNSUPPORTED = -2,  /* geometry the library has no kernel for       */
   QH_E_WORKSPACE = -3,    /* workspace missing or too small                  */
   QH_E_HIP = -4           /* a HIP runtime call failed       -> RuntimeError */
 };

@@ -391,7 +391,7 @@ class KVArena:
         import torch
         self.torch = torch
         if sliding_window or n_sliding_pages or tuple(sliding_layers):
-            raise ValueError("sliding-window pools are not part of this build")
+            raise ValueError("quail_amd has no sliding-window pools")
         self.dtype = dtype or torch.bfloat16
         self.device = device
         shapes = ([(n_kv, d_head)] * n_layers if layer_kv is None
@@ -435,7 +435,7 @@ class KVArena:
     def resize(self, n_pages: int, n_sliding_pages: int = 0, *,
                free_resident: bool = False) -> None:
         if n_sliding_pages:
-            raise ValueError("sliding-window pools are not part of this build")
+            raise ValueError("quail_amd has no sliding-window pools")
         if free_resident:
             self.drop_holds()
             for key in self.resident_keys():
@@ -474,7 +474,7 @@ class KVArena:
             if n < 64:
                 return tuple(evicted)
 
-    # ---- window API (no sliding layers in this build) -----------------
+    # ---- window API (no sliding layers in quail_amd) ----------------
 
     @property
     def has_sliding(self) -> bool:

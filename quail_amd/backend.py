@@ -286,29 +286,29 @@ class QuailBackend:
     def plan(self, region, context):
         """ModelBackend.plan (base.py:62-67; backend.py:346-400). Planning -
         filter ordering, join search, prefix-sharing and tree-attention
-        rules - is the reference's planner (quail/planner), which this
-        executor build does not carry; it executes the physical nodes that
+        rules - is the reference's planner (quail/planner), which quail_amd
+        does not carry; it executes the physical nodes that
         planner produces. Raises NotImplementedError."""
         raise NotImplementedError(
-            "QuailBackend.plan: this build carries the executor, not the planner "
+            "QuailBackend.plan: quail_amd carries the executor, not the planner "
             "(quail/planner); plan with the reference's QuailBackend.plan and run its "
             "AiFilter/AiJoin nodes through QuailBackend().start(GpuContext).execute(node, inputs)")
 
     def prepare_request(self, context) -> None:
         """Boot ahead of a request (backend.py:466-468): part of the request
-        runner, which this build does not carry. Raises NotImplementedError."""
+        runner, which quail_amd does not carry. Raises NotImplementedError."""
         raise NotImplementedError(
             "QuailBackend.prepare_request: the request runner (worker.py) is not part of "
-            "this build; start(GpuContext) boots the GPU")
+            "quail_amd; start(GpuContext) boots the GPU")
 
     def execute_request(self, context):
         """ModelBackend.execute_request (base.py:69-75; backend.py:470-472):
         the compute-process request runner (worker.py, graph.py) around the
-        executor, which this build does not carry. Raises
+        executor, which quail_amd does not carry. Raises
         NotImplementedError."""
         raise NotImplementedError(
             "QuailBackend.execute_request: the request runner (worker.py, graph.py) is not "
-            "part of this build; run each node with "
+            "part of quail_amd; run each node with "
             "QuailBackend().start(GpuContext).execute(node, inputs)")
 
 

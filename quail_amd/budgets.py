@@ -57,7 +57,7 @@ def arena_bytes(model: ModelSpec, device: DeviceSpec, chunk_tokens: int) -> floa
 
 
 def arena_pages(model: ModelSpec, device: DeviceSpec, chunk_tokens=None):
-    """(every-token pages, sliding pages); no sliding layers in this build."""
+    """(every-token pages, sliding pages); no sliding layers here."""
     if chunk_tokens is None:
         chunk_tokens = chunk_budget(model, device)
     free = arena_bytes(model, device, chunk_tokens)

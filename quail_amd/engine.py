@@ -37,10 +37,10 @@ class Engine:
         n_q, n_kv, head_dim: head geometry.
         rotary: object with cos_sin_cache ([max_pos, head_dim] bf16, cos|sin).
         fp8: whether linears are fp8 block-quantized. bf16 linears (the
-            reference's rerankers) are not part of this build: False raises.
+            reference's rerankers) are not part of quail_amd: False raises.
         kernels: "quail", the fused kernel set. The reference's "vllm"
             ablation set (attention.py:690-723) is not built here and raises.
-    Options of this build:
+    Options of quail_amd's engine:
         ue8m0: round activation scales up to powers of two (DeepGEMM's
             UE8M0 mode, attention.py:115); fp32 scales otherwise.
         gemm_hook: optional callable(name, M, N, K, launch) wrapping GEMM
@@ -69,13 +69,13 @@ class Engine:
         if kernels not in ("quail", "vllm"):
             raise ValueError(f"kernels must be 'quail' or 'vllm', got {kernels!r}")
         if kernels == "vllm":
-            raise ValueError("the unfused vLLM kernel set is not part of this build; "
+            raise ValueError("the unfused vLLM kernel set is not part of quail_amd; "
                              "use kernels='quail'")
         if tree_kernel not in ("fused", "resident", "two_pass"):
             raise ValueError("tree_kernel must be 'fused', 'resident' or 'two_pass', "
                              f"got {tree_kernel!r}")
         if not fp8:
-            raise ValueError("this build runs fp8 block-scaled linears only")
+            raise ValueError("quail_amd runs fp8 block-scaled linears only")
         self.kernels = kernels
         self.tree_kernel = tree_kernel
         self.fuse_kv_write = bool(fuse_kv_write)
@@ -168,7 +168,7 @@ class Engine:
         return q, k
 
     def qkv_attention(self, qkv, positions, attn, chunk):
-        """qk_norm_rope then attention, as one step of this build's pipeline.
+        """qk_norm_rope then attention, as one step of quail_amd's pipeline.
         On the unified path, where every chunk row is written to the arena,
         the norm/RoPE kernel writes k and v into the layer's pages itself (no
         k/v rows, no separate scatter); the result is bit-identical to the
@@ -289,7 +289,7 @@ class Engine:
         over retained and current KV (attention.py:878-953). Returns the bf16
         output, (rows, heads * dim)."""
         if window is not None:
-            raise ValueError("sliding-window attention is not part of this build")
+            raise ValueError("quail_amd has no sliding-window attention")
         scale = self.softmax_scale if softmax_scale is None else float(softmax_scale)
         n = q3.shape[0]
         layer = meta["layer"]

@@ -1,7 +1,7 @@
 """Physical KV page layout of the arena, and its logical-row views.
 
 The reference numbers arena rows page * page_tokens + slot and keeps each
-layer's pool as (rows, n_kv, d) (arena.py:343-353, :519-523). This build
+layer's pool as (rows, n_kv, d) (arena.py:343-353, :519-523). quail_amd
 keeps that numbering bit-exactly but stores, per layer,
 
   K: [n_pages, n_kv, page_tokens, d]   one 4 KiB block per (page, KV head)

@@ -170,7 +170,7 @@ class ChunkBuilder:
         return out
 
     def host_arrays(self):
-        """Every built array, copied out of the builder: {name: ndarray}, and
+        """Every built array, copied out of the chunk builder: {name: ndarray}, and
         the one buffer they all live in (16-byte aligned slots)."""
         _host.call("qp_chunk_arrays", self._native.ptr, self._arrays.ctypes.data)
         total = _host.call("qp_chunk_emit", self._native.ptr, None, 0,
@@ -302,7 +302,7 @@ def pack_chunk(torch, arena, groups, timing=None, pinned=True, *, attention_mode
         raise ValueError(f"attention_mode must be one of {ATTENTION_PATHS}, "
                          f"got {attention_mode!r}")
     if tuple(canvas):
-        raise ValueError("canvas rows belong to diffusion models, not this build")
+        raise ValueError("canvas rows belong to diffusion models, which quail_amd does not run")
     clock = _Clock(timing)
     tokens = TokenTable()
     builder = ChunkBuilder()
@@ -713,7 +713,7 @@ class _Join:
         return rows
 
     def stage(self, groups):
-        """Activate fresh anchors' pages and add every group's rows to the builder."""
+        """Activate fresh anchors' pages and add every group's rows to the chunk builder."""
         arena, sched, b = self.arena, self.sched, self.builder
         borrowing = sched.borrowing
         b.reset()
@@ -910,7 +910,7 @@ def run_join(torch, arena, pipeline, async_ans, anchor_prefixes, stage_suffixes,
     if len(keys) != len(prefixes):
         raise ValueError("anchor_keys must match anchor_prefixes")
     if tuple(getattr(pipeline, "canvas_ids", ())):
-        raise ValueError("canvas rows belong to diffusion models, not this build")
+        raise ValueError("canvas rows belong to diffusion models, which quail_amd does not run")
     frames = stage_frames or [[] for _ in range(k)]
     if k == 0:
         return [], [], 0

@@ -59,7 +59,7 @@ def _whole_pages(page_cost, page_tokens):
     for t in (0, 1, page_tokens - 1, page_tokens, page_tokens + 1, 7 * page_tokens + 3, 4097):
         if page_cost(t, None) != pages_for(t, page_tokens):
             raise ValueError("page_cost must price whole pages of page_tokens "
-                             "(sliding-window pricing is not part of this build)")
+                             "(quail_amd has no sliding-window pricing)")
 
 
 def _tree_arrays(tree, n):

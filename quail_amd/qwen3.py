@@ -37,7 +37,7 @@ class Qwen3Pipeline(ModelPipeline):
                  engine_class=Engine, **engine_options):
         """The reference's constructor (models/qwen3.py:21-38); engine_options
         (ue8m0, gemm_hook, attention_hook, tree_kernel, fuse_kv_write,
-        fuse_qkv_epilogue) go to this build's Engine."""
+        fuse_qkv_epilogue) go to quail_amd's Engine."""
         import torch
         self.layers = model.model.layers
         self.embed = model.model.embed_tokens

@@ -1,5 +1,5 @@
 """The drop-in boundary on the CPU: the reference's callers construct and
-call this build's Engine, pipeline and backend without changes.
+call quail_amd's Engine, pipeline and backend without changes.
 
 - Engine is built exactly the way the reference's Qwen3Pipeline builds it
   (quail/backends/quail/executor/models/qwen3.py:26-29: positional arena,

@@ -1,4 +1,4 @@
-"""The reference's forward loop drives this build's Engine (MI355X only).
+"""The reference's forward loop drives quail_amd's Engine (MI355X only).
 
 reference_call_sequence() issues the Engine calls the reference's
 Qwen3Pipeline.forward_chunk makes (quail/backends/quail/executor/models/
@@ -6,7 +6,7 @@ qwen3.py:46-77), in its order and with its arguments: embedding, norm_quant,
 gemm, qk_norm_rope -> (q, k), v as a strided view of the qkv output,
 attention(q, k, v, chunk), gemm, norm_quant with the residual, gemm of
 gate_up, activation_quant, gemm of down, index_select of the final rows and
-fused_add_rms_norm. This build's own pipeline fuses several of those steps
+fused_add_rms_norm. quail_amd's own pipeline fuses several of those steps
 (q/k norm + RoPE writing the arena, gate_up + SiLU + quant, gather + final
 norm); every fusion is bit-identical to its parts, so the two loops must
 produce identical final rows, on both attention paths.

@@ -907,7 +907,7 @@ def test_qwen3_4b_decisions_over_1024_rows_agree_within_the_oracle_floor():
     has one); and its overall agreement is within three binomial standard
     deviations of the pair's. Taking any one of those families from the
     oracle instead leaves the agreement within a few rows of the GPU's
-    (a builder run: GEMMs 913, attention 919, norms 920 against the GPU's
+    (a separate run of the same rows: GEMMs 913, attention 919, norms 920 against the GPU's
     915 of 1,024), so no single stage dominates."""
     from e2e_support import decision_stats, describe
 
