@@ -133,6 +133,17 @@ int64_t qp_tokens_add_flat(void* tokens, const void* data, int32_t elem_bytes, i
                            const int64_t* offsets);
 int64_t qp_tokens_length(const void* tokens, int64_t entry);
 
+/* The prefix tree of n documents (prefix_tree, quail/execution/tokens.py:547-591)
+ * over one flat buffer of ids of elem_bytes = 4 or 8 bytes: document i is
+ * ids[offsets[i] .. offsets[i+1]) (n + 1 offsets, in ids). Writes order[n]
+ * (documents in ascending order of their ids' big-endian int32 bytes, equal
+ * documents in input order), parent[n] (the document each borrows from, -1
+ * for none) and shared[n] (borrowed tokens: the common prefix with the
+ * sorted predecessor, capped one short of the document's length, floored to
+ * page_tokens). */
+int qp_prefix_tree(const void* ids, int32_t elem_bytes, int64_t n, const int64_t* offsets,
+                   int64_t page_tokens, int64_t* order, int64_t* parent, int64_t* shared);
+
 /* ------------------------------------------------------------------------
  * Chunk builder: pack_chunk (loop.py:219-577). Groups are added in chunk
  * order; build() lays out every array of the chunk's Chunk.meta.

@@ -77,6 +77,7 @@ SIGNATURES = {
     "qp_tokens_add": (_i64, [_p, _p, _p, _p, _i32]),
     "qp_tokens_add_flat": (_i64, [_p, _p, _i32, _i64, _p]),
     "qp_tokens_length": (_i64, [_p, _i64]),
+    "qp_prefix_tree": (ctypes.c_int, [_p, _i32, _i64, _p, _i64, _p, _p, _p]),
     "qp_chunk_new": (_p, []),
     "qp_chunk_delete": (None, [_p]),
     "qp_chunk_reset": (ctypes.c_int, [_p]),

@@ -18,7 +18,7 @@ from quail_amd.model import SYNTHETIC_FALSE_IDS, SYNTHETIC_TRUE_IDS
 from quail_amd.qwen3 import Qwen3Pipeline
 from quail_amd.readout import AnswerRows, AsyncAnswers
 from quail_amd.specs import MI355X
-from quail_amd.tokens import chain_tokens, prefix_tree
+from quail_amd.tokens import chain_tokens, flat_tokens, prefix_tree
 
 
 def lognormal_lengths(n, median, mean, cap, rng):
@@ -54,20 +54,49 @@ def synthetic_filter_workload(n_rows, *, prefix_tokens=64, median=180, mean=230,
 class RowPrompts:
     """Row i = instruction + document i (tokens.DocumentPrefixes).
 
-    In-memory documents are materialised once; documents read from a token
-    store stay views of the mapped file, chained after the instruction.
+    Rows read from a token store are chains of the instruction and a view of
+    the mapped file, built on access; other rows are views of one buffer of
+    every row's ids, built once. flat_tokens() hands that buffer (for a
+    store, built on first call) to the prefix tree and the packer's token
+    table, which read all rows at once.
     """
 
     def __init__(self, instruction, documents):
-        instruction = np.asarray(instruction, dtype=np.int64)
-        self.rows = [chain_tokens(instruction, d) if hasattr(d, "token_parts")
-                     else np.concatenate([instruction, d]) for d in documents]
+        self.instruction = np.asarray(instruction, dtype=np.int64).reshape(-1)
+        self.documents = documents
+        self._stored = len(documents) > 0 and hasattr(documents[0], "token_parts")
+        self._flat = None if self._stored else flat_tokens(documents, self.instruction)
 
     def __len__(self):
-        return len(self.rows)
+        return len(self.documents)
 
     def __getitem__(self, i):
-        return self.rows[i]
+        if self._stored:
+            return chain_tokens(self.instruction, self.documents[i])
+        ids, offsets = self._flat
+        if i < 0:
+            i += len(self)
+        if not 0 <= i < len(self):
+            raise IndexError(i)
+        return ids[offsets[i]:offsets[i + 1]]
+
+    @property
+    def rows(self):
+        return [self[i] for i in range(len(self))]
+
+    def lengths(self):
+        """Every row's token count (int64 array)."""
+        if self._flat is not None:
+            return np.diff(self._flat[1])
+        if hasattr(self.documents, "lengths"):
+            return self.documents.lengths.numpy() + self.instruction.size
+        return np.fromiter((len(d) for d in self.documents), dtype=np.int64,
+                           count=len(self.documents)) + self.instruction.size
+
+    def flat_tokens(self):
+        if self._flat is None:
+            self._flat = flat_tokens(self.documents, self.instruction)
+        return self._flat
 
 
 class FilterRunner:
@@ -128,7 +157,7 @@ class FilterRunner:
         wall = time.perf_counter() - t0
         if self.arena.accounting.owned:
             raise AssertionError("the filter left pages resident")
-        input_tokens = sum(len(d) + len(tail) for d in docs.rows)
+        input_tokens = int(docs.lengths().sum()) + len(tail) * len(docs)
         stats.update(wall_s=wall, fresh_tokens=tokens, input_tokens=input_tokens,
                      rows=len(docs), shared_tokens=tree.shared_tokens)
         self.last = stats

@@ -328,6 +328,14 @@ int64_t qp_tokens_length(const void* tokens, int64_t entry) {
   });
 }
 
+int qp_prefix_tree(const void* ids, int32_t elem_bytes, int64_t n, const int64_t* offsets,
+                   int64_t page_tokens, int64_t* order, int64_t* parent, int64_t* shared) {
+  return (int)guarded([&] {
+    prefix_tree(ids, elem_bytes, n, offsets, page_tokens, order, parent, shared);
+    return (int64_t)kOk;
+  });
+}
+
 // ---- chunk builder -------------------------------------------------------------
 
 void* qp_chunk_new(void) { return new (std::nothrow) ChunkBuilder(); }

@@ -172,6 +172,13 @@ class TokenTable {
   std::vector<TokenPart> parts_;
 };
 
+// The prefix tree of n documents held in one flat buffer of int32 or int64
+// ids (document i = ids[offsets[i] .. offsets[i+1])): order[k] is the k-th
+// document in sorted order, parent[d] the document d borrows from (-1:
+// none), shared[d] the tokens it borrows, a multiple of page_tokens.
+void prefix_tree(const void* ids, int32_t elem_bytes, int64_t n, const int64_t* offsets,
+                 int64_t page_tokens, int64_t* order, int64_t* parent, int64_t* shared);
+
 // ----------------------------------------------------------------------------
 // Admission.
 

@@ -86,18 +86,29 @@ class TokenTable:
         self.extend(sequences)
 
     def extend(self, sequences):
-        """Add many sequences at once, copied into one flat int64 buffer."""
-        arrays = [token_array(seq) for seq in sequences]
-        if not arrays:
+        """Add many sequences at once over one flat buffer: the one a source
+        with flat_tokens() (RowPrompts, TokenStore) already holds, else one
+        int64 copy."""
+        if hasattr(sequences, "flat_tokens"):
+            flat, offsets = sequences.flat_tokens()
+            if flat.dtype not in (np.int32, np.int64) or not flat.flags.c_contiguous:
+                flat = np.ascontiguousarray(flat, dtype=np.int64)
+            offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+            lengths = np.diff(offsets)
+        else:
+            arrays = [token_array(seq) for seq in sequences]
+            lengths = np.fromiter((a.size for a in arrays), dtype=np.int64, count=len(arrays))
+            flat = np.concatenate(arrays).astype(np.int64, copy=False) if lengths.sum() else \
+                np.zeros(1, dtype=np.int64)
+            offsets = np.zeros(len(arrays) + 1, dtype=np.int64)
+            np.cumsum(lengths, out=offsets[1:])
+        if not lengths.size:
             return
-        lengths = np.fromiter((a.size for a in arrays), dtype=np.int64, count=len(arrays))
-        flat = np.concatenate(arrays).astype(np.int64, copy=False) if lengths.sum() else \
-            np.zeros(1, dtype=np.int64)
-        offsets = np.zeros(len(arrays) + 1, dtype=np.int64)
-        np.cumsum(lengths, out=offsets[1:])
-        self._keep.append(flat)
-        _host.call("qp_tokens_add_flat", self._native.ptr, flat.ctypes.data, 8, len(arrays),
-                   offsets.ctypes.data)
+        if not flat.size:
+            flat = np.zeros(1, dtype=flat.dtype)
+        self._keep.append((flat, offsets))
+        _host.call("qp_tokens_add_flat", self._native.ptr, flat.ctypes.data, flat.itemsize,
+                   lengths.size, offsets.ctypes.data)
         self._lengths.extend(lengths.tolist())
 
     @property

@@ -43,38 +43,84 @@ class PrefixTree:
         return sum(self.shared)
 
 
-def _ids(doc):
-    if isinstance(doc, np.ndarray):
-        return doc.astype(np.int64, copy=False)
-    return token_array(doc).astype(np.int64, copy=False)
+def _integer_ids(seq):
+    """A sequence's ids as a 1-D integer array; TypeError if they are not
+    integers (a test tokenizer's words)."""
+    a = token_array(seq)
+    if a.size == 0:
+        return np.empty(0, dtype=np.int32)
+    if a.dtype.kind not in "iu":
+        raise TypeError(f"token ids of dtype {a.dtype}")
+    return a.reshape(-1)
 
 
-def _common(a, b) -> int:
-    n = min(a.size, b.size)
-    diff = np.flatnonzero(a[:n] != b[:n])
-    return int(diff[0]) if diff.size else n
+def flat_tokens(documents, prefix=None):
+    """Every document's ids in one buffer: (ids, offsets) with document i at
+    ids[offsets[i]:offsets[i+1]], each preceded by `prefix` if given. The ids
+    are int32 when every source part is, else int64. A source with its own
+    flat_tokens() (RowPrompts, TokenStore) hands over its buffer; otherwise
+    each document is read once. TypeError for ids that are not integers."""
+    p = None if prefix is None else _integer_ids(np.asarray(prefix))
+    if hasattr(documents, "flat_tokens"):
+        ids, offsets = documents.flat_tokens()
+        return (ids, offsets) if p is None else _prefixed(p, ids, offsets)
+    arrays = [_integer_ids(documents[i]) for i in range(len(documents))]
+    lengths = np.fromiter((a.size for a in arrays), dtype=np.int64, count=len(arrays))
+    offsets = np.zeros(len(arrays) + 1, dtype=np.int64)
+    np.cumsum(lengths + (0 if p is None else p.size), out=offsets[1:])
+    narrow = all(a.dtype == np.int32 for a in arrays) and (p is None or _fits_int32(p))
+    dtype = np.int32 if narrow else np.int64
+    if p is not None:
+        p = p.astype(dtype, copy=False)
+        arrays = [x for a in arrays for x in (p, a)]
+    ids = np.concatenate(arrays).astype(dtype, copy=False) if arrays else \
+        np.empty(0, dtype=dtype)
+    return ids, offsets
 
 
-def prefix_tree(documents, page_tokens: int) -> PrefixTree:
-    """The prefix tree of a document set (tokens.py:547-591).
+def _fits_int32(a):
+    return a.dtype == np.int32 or not a.size or (
+        int(a.min()) >= -2**31 and int(a.max()) < 2**31)
 
-    Documents are visited in the order of their token ids as big-endian
-    int32 bytes. Each one shares with its predecessor in that order the
-    longest common prefix, capped one token short of its own length and
-    rounded down to whole pages; a document that shares a page or more hangs
-    under the nearest document on its predecessor's root path whose own
-    shared length is below that (or the path's root). The root path is kept
-    as a stack, so each document is pushed and popped once."""
+
+def _prefixed(prefix, ids, offsets):
+    """(ids, offsets) of documents given as (ids, offsets), each preceded by
+    the integer array prefix, built with array operations (no per-document
+    work)."""
+    n = offsets.size - 1
+    lengths = np.diff(offsets)
+    p = prefix.size
+    out_offsets = np.zeros(n + 1, dtype=np.int64)
+    np.cumsum(lengths + p, out=out_offsets[1:])
+    narrow = ids.dtype == np.int32 and _fits_int32(prefix)
+    out = np.empty(int(out_offsets[-1]), dtype=np.int32 if narrow else np.int64)
+    is_doc = np.ones(out.size, dtype=bool)
+    if p and n:
+        at = (out_offsets[:-1, None] + np.arange(p, dtype=np.int64)).reshape(-1)
+        is_doc[at] = False
+        out[at] = np.tile(prefix.astype(out.dtype, copy=False), n)
+    out[is_doc] = ids[int(offsets[0]):int(offsets[-1])] if n else ids[:0]
+    return out, out_offsets
+
+
+def _prefix_tree_items(documents, page_tokens):
+    """prefix_tree for tokens that are not integers (tokens.py:560-564):
+    sorted as tuples, the common prefix counted item by item."""
     n = len(documents)
-    ids = [_ids(documents[i]) for i in range(n)]
-    order = sorted(range(n), key=lambda i: ids[i].astype(">i4").tobytes())
-    parent = [None] * n
-    shared = [0] * n
-    path = []  # root path of the document visited last, root first
+    items = [tuple(documents[i]) for i in range(n)]
+
+    def common(a, b):
+        k = 0
+        while k < min(len(a), len(b)) and a[k] == b[k]:
+            k += 1
+        return k
+
+    order = sorted(range(n), key=items.__getitem__)
+    parent, shared, path = [None] * n, [0] * n, []
     for prev, doc in zip([None] + order[:-1], order):
         pages = 0
         if prev is not None:
-            keep = min(_common(ids[prev], ids[doc]), max(ids[doc].size - 1, 0))
+            keep = min(common(items[prev], items[doc]), max(len(items[doc]) - 1, 0))
             pages = keep // page_tokens * page_tokens
         if not pages:
             path = [doc]
@@ -85,6 +131,35 @@ def prefix_tree(documents, page_tokens: int) -> PrefixTree:
         shared[doc] = pages
         path.append(doc)
     return PrefixTree(order, parent, shared)
+
+
+def prefix_tree(documents, page_tokens: int) -> PrefixTree:
+    """The prefix tree of a document set (tokens.py:547-591), built by the
+    host library (qp_prefix_tree) over the documents' ids in one buffer.
+
+    Documents are visited in the order of their token ids as big-endian
+    int32 bytes. Each one shares with its predecessor in that order the
+    longest common prefix, capped one token short of its own length and
+    rounded down to whole pages; a document that shares a page or more hangs
+    under the nearest document on its predecessor's root path whose own
+    shared length is below that (or the path's root)."""
+    if page_tokens <= 0:
+        raise ValueError(f"page_tokens must be positive, got {page_tokens}")
+    try:
+        ids, offsets = flat_tokens(documents)
+    except (TypeError, ValueError):
+        return _prefix_tree_items(documents, page_tokens)
+    from . import _host
+    n = offsets.size - 1
+    ids = np.ascontiguousarray(ids)
+    offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+    order = np.empty(n, dtype=np.int64)
+    parent = np.empty(n, dtype=np.int64)
+    shared = np.empty(n, dtype=np.int64)
+    _host.call("qp_prefix_tree", ids.ctypes.data, ids.itemsize, n, offsets.ctypes.data,
+               page_tokens, order.ctypes.data, parent.ctypes.data, shared.ctypes.data)
+    return PrefixTree(order.tolist(), [None if p < 0 else p for p in parent.tolist()],
+                      shared.tolist())
 
 
 def shared_prefix_lengths(sequences) -> list:
@@ -469,6 +544,27 @@ class TokenStore:
 
     def select(self, indices):
         return TokenSelection(self.path, indices)
+
+    def flat_tokens(self):
+        """Every document's ids as (ids, offsets) over one buffer: the mapped
+        values themselves when the file holds one record batch, else one
+        concatenation of the batches' values."""
+        parts, offsets, base = [], [np.zeros(1, dtype=np.int64)], 0
+        for docs in self._docs:
+            for offs, values in zip(docs.piece_offsets, docs.piece_values):
+                lo, hi = int(offs[0]), int(offs[-1])
+                parts.append(values.to_numpy(zero_copy_only=True)[lo:hi])
+                offsets.append(offs[1:].astype(np.int64) - lo + base)
+                base += hi - lo
+        if not parts:
+            return np.empty(0, dtype=np.int32), offsets[0]
+        if len(parts) == 1:
+            ids = parts[0]
+        else:
+            wide = any(p.dtype != np.int32 for p in parts)
+            ids = np.concatenate([p.astype(np.int64 if wide else np.int32, copy=False)
+                                  for p in parts])
+        return ids, np.concatenate(offsets)
 
     def close(self):
         self._source.close()

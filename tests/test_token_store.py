@@ -237,6 +237,45 @@ def test_join_from_a_token_store_packs_the_reference_chunks(tmp_path, sc):
     assert total == want["tokens"] and stats["borrowed_tokens"] == want["borrowed"]
 
 
+@pytest.mark.parametrize("batch_rows,token_type", [(4096, None), (7, None), (5, "int64")])
+def test_flat_tokens_of_a_store_and_its_row_prompts(tmp_path, batch_rows, token_type):
+    """A store's flat buffer is its documents in order (the mapped values
+    themselves for one record batch); RowPrompts over it adds the
+    instruction to every row, and the packer's token table reads the same
+    lengths from it."""
+    docs = _docs(6, n=30)
+    tt = None if token_type is None else pa.int64()
+    store = TokenStore.from_documents(str(tmp_path / "t.arrow"), docs, batch_rows=batch_rows,
+                                      token_type=tt)
+    ids, offsets = store.flat_tokens()
+    assert offsets.tolist() == np.concatenate([[0], np.cumsum([d.size for d in docs])]).tolist()
+    assert np.array_equal(ids.astype(np.int64), np.concatenate(docs))
+    if batch_rows >= len(docs) and token_type is None:
+        assert np.shares_memory(ids, store[0].numpy())
+    instruction = np.arange(4, dtype=np.int64) + 10
+    rows = RowPrompts(instruction, store)
+    ids, offsets = rows.flat_tokens()
+    for i, d in enumerate(docs):
+        assert np.array_equal(ids[offsets[i]:offsets[i + 1]].astype(np.int64),
+                              np.concatenate([instruction, d]))
+    assert rows.lengths().tolist() == [d.size + 4 for d in docs]
+    table = loop.TokenTable(rows)
+    assert [table.length(i) for i in range(len(docs))] == [d.size + 4 for d in docs]
+
+
+def test_row_prompts_of_arrays_are_views_of_one_buffer():
+    docs = _docs(8, n=12)
+    instruction = np.array([5, 6], dtype=np.int64)
+    rows = RowPrompts(instruction, docs)
+    ids, offsets = rows.flat_tokens()
+    for i, d in enumerate(docs):
+        assert np.shares_memory(rows[i], ids) or rows[i].size == 0
+        assert np.array_equal(rows[i], np.concatenate([instruction, d]))
+    assert np.array_equal(rows[-1], rows[len(docs) - 1])
+    with pytest.raises(IndexError):
+        rows[len(docs)]
+
+
 def test_row_prompts_chain_stored_documents(tmp_path):
     """Rows over a token store are instruction + document chains over the
     mapped buffer (tokens.py:412-429), equal to the materialised rows."""

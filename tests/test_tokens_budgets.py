@@ -11,11 +11,12 @@ import json
 import os
 from dataclasses import replace
 
+import numpy as np
 import pytest
 
 from quail_amd import budgets
 from quail_amd.specs import H100_SXM, MI355X, QWEN3_4B_FP8, QWEN3_32B_FP8
-from quail_amd.tokens import DocumentPrefixes, prefix_tree
+from quail_amd.tokens import DocumentPrefixes, _prefix_tree_items, flat_tokens, prefix_tree
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 TREE_CASES = json.load(open(os.path.join(HERE, "golden", "prefix_tree_cases.json")))["cases"]
@@ -53,6 +54,62 @@ def test_prefix_tree_sorts_ids_as_big_endian_int32():
     # 256 sorts after 1 even though its low byte is 0
     tree = prefix_tree([[256, 5], [1, 9], [255, 0]], 16)
     assert tree.order == [1, 2, 0]
+
+
+def test_prefix_tree_orders_by_unsigned_big_endian_bytes():
+    """Negative ids and ids of 2^31 and up sort by their int32 bytes read as
+    unsigned big-endian numbers: 0 < 5 < 2^31 (0x80000000) < -1 (0xFFFFFFFF);
+    a proper prefix sorts before its extensions, equal documents keep their
+    input order."""
+    tree = prefix_tree([[-1], [5], [2**31], [0], [5, 0], [5]], 16)
+    assert tree.order == [3, 1, 5, 4, 2, 0]
+    tree = prefix_tree(np.array([[-1], [5], [2**31], [0]], dtype=np.int64).tolist(), 16)
+    assert tree.order == [3, 1, 2, 0]
+
+
+def test_prefix_tree_of_words_sorts_them_as_tuples():
+    """Tokens that are not integers (a test tokenizer's words) take the
+    tuple order and item-by-item common prefix (tokens.py:556-564)."""
+    words = [["b"] * 20, ["a"] * 20, ["a"] * 17 + ["c"]]
+    tree = prefix_tree(words, 16)
+    assert tree.order == [1, 2, 0]
+    assert tree.parent == [None, None, 1] and tree.shared == [0, 0, 16]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_native_prefix_tree_matches_the_item_restatement(seed):
+    """Random documents over a small alphabet (long shared prefixes,
+    duplicates, empty documents, pages of 1, 4 and 16): the host library's
+    tree equals the pure-Python one on the same ids, int32 and int64, as
+    lists and as one flat buffer."""
+    rng = np.random.default_rng(seed)
+    stems = [rng.integers(0, 3, size=int(rng.integers(0, 70))) for _ in range(6)]
+    docs = []
+    for _ in range(120):
+        stem = stems[int(rng.integers(0, len(stems)))]
+        cut = int(rng.integers(0, stem.size + 1))
+        docs.append(np.concatenate([stem[:cut], rng.integers(0, 3, size=int(rng.integers(0, 20)))]))
+    for page in (1, 4, 16):
+        want = _prefix_tree_items([d.tolist() for d in docs], page)
+        for dtype in (np.int32, np.int64):
+            got = prefix_tree([d.astype(dtype) for d in docs], page)
+            assert (got.order, got.parent, got.shared) == (want.order, want.parent, want.shared)
+
+
+def test_flat_tokens_with_a_prefix_equals_the_rows():
+    rng = np.random.default_rng(3)
+    docs = [rng.integers(0, 1000, size=int(rng.integers(0, 9)), dtype=np.int32)
+            for _ in range(50)]
+    for prefix in ([], [7, 8, 9], np.array([2**31 + 1], dtype=np.int64)):
+        ids, offsets = flat_tokens(docs, prefix)
+        assert offsets[0] == 0 and offsets.size == len(docs) + 1
+        for i, d in enumerate(docs):
+            want = np.concatenate([np.asarray(prefix, dtype=np.int64), d.astype(np.int64)])
+            assert np.array_equal(ids[offsets[i]:offsets[i + 1]].astype(np.int64), want)
+        assert ids.dtype == (np.int64 if np.max(np.asarray(prefix, dtype=np.int64),
+                                                initial=0) >= 2**31 else np.int32)
+    ids, offsets = flat_tokens([], [1, 2])
+    assert ids.size == 0 and offsets.tolist() == [0]
 
 
 def test_document_prefixes_prepend_the_instruction():
