@@ -18,7 +18,7 @@ from quail_amd.model import SYNTHETIC_FALSE_IDS, SYNTHETIC_TRUE_IDS
 from quail_amd.qwen3 import Qwen3Pipeline
 from quail_amd.readout import AnswerRows, AsyncAnswers
 from quail_amd.specs import MI355X
-from quail_amd.tokens import chain_tokens, flat_tokens, prefix_tree
+from quail_amd.tokens import _Rows, chain_tokens, flat_tokens, prefix_tree
 
 
 def lognormal_lengths(n, median, mean, cap, rng):
@@ -51,7 +51,7 @@ def synthetic_filter_workload(n_rows, *, prefix_tokens=64, median=180, mean=230,
     return instruction, documents, tail
 
 
-class RowPrompts:
+class RowPrompts(_Rows):
     """Row i = instruction + document i (tokens.DocumentPrefixes).
 
     Rows read from a token store are chains of the instruction and a view of
@@ -70,14 +70,10 @@ class RowPrompts:
     def __len__(self):
         return len(self.documents)
 
-    def __getitem__(self, i):
+    def row(self, i):
         if self._stored:
             return chain_tokens(self.instruction, self.documents[i])
         ids, offsets = self._flat
-        if i < 0:
-            i += len(self)
-        if not 0 <= i < len(self):
-            raise IndexError(i)
         return ids[offsets[i]:offsets[i + 1]]
 
     @property

@@ -263,7 +263,7 @@ def test_flat_tokens_of_a_store_and_its_row_prompts(tmp_path, batch_rows, token_
     assert [table.length(i) for i in range(len(docs))] == [d.size + 4 for d in docs]
 
 
-def test_row_prompts_of_arrays_are_views_of_one_buffer():
+def test_row_prompts_of_arrays_are_views_of_one_buffer(tmp_path):
     docs = _docs(8, n=12)
     instruction = np.array([5, 6], dtype=np.int64)
     rows = RowPrompts(instruction, docs)
@@ -274,6 +274,14 @@ def test_row_prompts_of_arrays_are_views_of_one_buffer():
     assert np.array_equal(rows[-1], rows[len(docs) - 1])
     with pytest.raises(IndexError):
         rows[len(docs)]
+    # slices give lists of rows, as the list of rows this replaces did
+    part = rows[2:5]
+    assert isinstance(part, list) and len(part) == 3
+    assert all(np.array_equal(a, rows[i]) for a, i in zip(part, range(2, 5)))
+    # a token store of prompt rows reads back the same rows
+    store = TokenStore.from_documents(str(tmp_path / "rows.arrow"), rows, batch_rows=5)
+    assert len(store) == len(rows)
+    assert all(np.array_equal(store[i].numpy(), rows[i]) for i in range(len(rows)))
 
 
 def test_row_prompts_chain_stored_documents(tmp_path):
