@@ -13,7 +13,13 @@ namespace qh {
 // attention.py:143-175 layer-0 path when residual == nullptr).
 // One wave per row; lane l's vector v covers columns (v*64 + l)*8 .. +8, so
 // lanes 16j..16j+15 of one vector hold one 128-wide group.
-template <int VPL>
+// FUSED: residual != nullptr; EXACT: H == VPL * 512 (no per-vector guards).
+// Both compile-time, so the kernel body is straight-line code: every load of
+// the row is issued first, and each wait leaves the later loads and the
+// residual stores in flight. With the loads next to the residual stores and
+// these flags tested at run time, a wave made ten dependent HBM round trips
+// per row and waited for its own stores (0.31 ms for 102,400 rows of 2560).
+template <int VPL, bool FUSED, bool EXACT>
 __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
     const uint16_t* __restrict__ x, long ldx, uint16_t* __restrict__ residual,
     long ld_res, const uint16_t* __restrict__ w, float eps, int T, int H,
@@ -21,32 +27,48 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  const int nvec = H >> 9;  // vectors of 8 per lane: H / 512
-  float v[VPL][8];
-  float ss = 0.f;
-  const bool fused = residual != nullptr;
+  const int nvec = EXACT ? VPL : H >> 9;  // vectors of 8 per lane: H / 512
+  bf16x8 xv[VPL], rv[VPL], wv[VPL];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     if (i < nvec) {
       const long col = ((long)i * 64 + lane) * 8;
-      bf16x8 xv = load8(x + (long)t * ldx + col);
-      if (fused) {
-        bf16x8 rv = load8(residual + (long)t * ld_res + col);
-        bf16x8 sum;
+      xv[i] = load8(x + (long)t * ldx + col);
+      if (FUSED) rv[i] = load8(residual + (long)t * ld_res + col);
+      wv[i] = load8(w + col);
+    }
+  }
+  float v[VPL][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    if (i < nvec) {
+      if (FUSED) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          float s = xv.get(e) + rv.get(e);
+          const float s = xv[i].get(e) + rv[i].get(e);
           v[i][e] = s;
-          sum.set(e, f32_to_bf16(s));
           ss += s * s;
         }
-        store8(residual + (long)t * ld_res + col, sum);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          v[i][e] = xv.get(e);
+          v[i][e] = xv[i].get(e);
           ss += v[i][e] * v[i][e];
         }
+      }
+    }
+  }
+  if (FUSED) {
+    // the new residual (x + residual, rounded to bf16)
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      if (i < nvec) {
+        const long col = ((long)i * 64 + lane) * 8;
+        bf16x8 sum;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum.set(e, f32_to_bf16(v[i][e]));
+        store8(residual + (long)t * ld_res + col, sum);
       }
     }
   }
@@ -56,16 +78,15 @@ __global__ __launch_bounds__(256) void add_rmsnorm_quant_kernel(
   for (int i = 0; i < VPL; ++i) {
     if (i < nvec) {
       const long col = ((long)i * 64 + lane) * 8;
-      bf16x8 wv = load8(w + col);
       float y[8];
       float amax = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        if (fused) {
-          y[e] = v[i][e] * rstd * wv.get(e);
+        if (FUSED) {
+          y[e] = v[i][e] * rstd * wv[i].get(e);
         } else {
           // vLLM rms_norm: bf16(bf16(x * rstd) * w)
-          y[e] = round_bf16(round_bf16(v[i][e] * rstd) * wv.get(e));
+          y[e] = round_bf16(round_bf16(v[i][e] * rstd) * wv[i].get(e));
         }
         amax = fmaxf(amax, fabsf(y[e]));
       }
@@ -566,9 +587,15 @@ extern "C" int qh_add_rmsnorm_quant(const void* x, long ldx, void* residual,
                        (const uint16_t*)x, ldx, (uint16_t*)residual, ld_res,
                        (const uint16_t*)w, eps, T, H, (uint8_t*)out_q, scales, ue8m0);
   };
-  if (vpl <= 5) args(add_rmsnorm_quant_kernel<5>);
-  else if (vpl <= 10) args(add_rmsnorm_quant_kernel<10>);
-  else args(add_rmsnorm_quant_kernel<16>);
+  const bool fused = residual != nullptr;
+  if (vpl == 5) fused ? args(add_rmsnorm_quant_kernel<5, true, true>)
+                      : args(add_rmsnorm_quant_kernel<5, false, true>);
+  else if (vpl == 10) fused ? args(add_rmsnorm_quant_kernel<10, true, true>)
+                            : args(add_rmsnorm_quant_kernel<10, false, true>);
+  else if (vpl < 10) fused ? args(add_rmsnorm_quant_kernel<10, true, false>)
+                           : args(add_rmsnorm_quant_kernel<10, false, false>);
+  else fused ? args(add_rmsnorm_quant_kernel<16, true, false>)
+             : args(add_rmsnorm_quant_kernel<16, false, false>);
   return launch_status("add_rmsnorm_quant");
 }
 
