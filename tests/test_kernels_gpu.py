@@ -45,7 +45,7 @@ def _check_quant(q_gpu, s_gpu, q_ref, s_ref, *, max_frac_off=2e-4, scale_rtol=1e
     assert frac <= max_frac_off, f"{frac:.2e} of fp8 codes differ"
 
 
-@pytest.mark.parametrize("H", [2560, 5120])
+@pytest.mark.parametrize("H", [1024, 2560, 5120, 8192])
 def test_add_rmsnorm_quant_fused_and_plain(H):
     g = _gen(1)
     T = 37
