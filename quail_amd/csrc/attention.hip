@@ -217,18 +217,36 @@ __device__ __forceinline__ int tile_seq(const int32_t* __restrict__ off, int n, 
 // sequence): its L2 then holds the K/V pages of its own KV heads only, and
 // the q-tiles of one sequence, which read the same pages, run there back to
 // back. Otherwise the head group is L % gy. Either way the map is a
-// bijection of [0, gx) x [0, gy).
+// bijection of [0, gx) x [0, gy). The launchers keep gx * gy below 2^31, so
+// L is a 32-bit index; per is a power of two for every head count in use
+// (8 and 16 head groups), which makes the map shifts and masks instead of a
+// scalar division routine ahead of the first load.
 __device__ __forceinline__ void xcd_item(int bx, int by, int gx, int gy, int& b, int& y) {
-  const long L = (long)by * gx + bx;
-  if (gy % 8 == 0) {
-    const int per = gy / 8;
-    const long r = L / 8;
-    y = (int)(L % 8) * per + (int)(r % per);
-    b = (int)(r / per);
+  const uint32_t L = (uint32_t)by * (uint32_t)gx + (uint32_t)bx;
+  if ((gy & 7) == 0) {
+    const uint32_t per = (uint32_t)gy >> 3;
+    const uint32_t r = L >> 3;
+    uint32_t rq, rr;
+    if ((per & (per - 1)) == 0) {
+      rq = r >> __builtin_ctz(per);
+      rr = r & (per - 1);
+    } else {
+      rq = r / per;
+      rr = r - rq * per;
+    }
+    y = (int)((L & 7) * per + rr);
+    b = (int)rq;
   } else {
-    y = (int)(L % gy);
-    b = (int)(L / gy);
+    y = (int)(L % (uint32_t)gy);
+    b = (int)(L / (uint32_t)gy);
   }
+}
+
+// x / d for wave-uniform x >= 0 and d > 0: a shift when d is a power of two
+// (the GQA group sizes in use), a division otherwise.
+__device__ __forceinline__ int udiv_uniform(int x, int d) {
+  return (d & (d - 1)) == 0 ? (int)((uint32_t)x >> __builtin_ctz((uint32_t)d))
+                            : (int)((uint32_t)x / (uint32_t)d);
 }
 
 template <bool CAUSAL>
@@ -256,9 +274,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
   const int i0 = tq * BQ;
   const int kv_len = p.kv_len[s];
 
-  const int group = p.n_q / p.n_kv;
+  const int group = udiv_uniform(p.n_q, p.n_kv);
   const int hq = hy * HPW + wave;
-  const int hk = (hy * HPW) / group;
+  const int hk = udiv_uniform(hy * HPW, group);
 
   // keys this tile reads: causal rows i attend keys < kv_len - count + i + 1
   int kv_end = kv_len;
@@ -553,9 +571,9 @@ __global__ __launch_bounds__(256, 3) void attn_paged_kernel(AttnParams p) {
   const int n_qt = (count + BQ - 1) / BQ;
   const int i0 = (n_qt - 1 - (b - p.tile_off[s])) * BQ;
   const int kv_len = p.kv_len[s];
-  const int group = p.n_q / p.n_kv;
+  const int group = udiv_uniform(p.n_q, p.n_kv);
   const int hq = hy * HPW + wave;
-  const int hk = (hy * HPW) / group;
+  const int hk = udiv_uniform(hy * HPW, group);
   int kv_end = kv_len;
   if (CAUSAL) kv_end = min(kv_len, kv_len - count + min(i0 + BQ, count));
   kv_end = max(kv_end, 0);
@@ -915,9 +933,9 @@ __global__ __launch_bounds__(256, 3) void attn_tree_kernel(TreeParams p) {
   const int count = p.cu_a[s + 1] - q0;
   const int n_qt = (count + BQ - 1) / BQ;
   const int i0 = (n_qt - 1 - (b - p.tile_off[s])) * BQ;
-  const int group = p.n_q / p.n_kv;
+  const int group = udiv_uniform(p.n_q, p.n_kv);
   const int hq = hy * HPW + wave;
-  const int hk = (hy * HPW) / group;
+  const int hk = udiv_uniform(hy * HPW, group);
   int r = p.seg_read[s];
   if (r >= p.n_reads) r = -1;
   const int node_keys = r >= 0 ? max(0, p.read_used[r]) : 0;
@@ -1318,9 +1336,9 @@ __global__ __launch_bounds__(512, 1) void attn_tree_node_kernel(TreeParams p) {
   const int hy = (int)blockIdx.x % n_hy;
   const int wj = (int)blockIdx.x / n_hy;
   if (wj >= W) return;
-  const int group = p.n_q / p.n_kv;
+  const int group = udiv_uniform(p.n_q, p.n_kv);
   const int hq = hy * HPW + (wave & 3);
-  const int hk = (hy * HPW) / group;
+  const int hk = udiv_uniform(hy * HPW, group);
   const long long C = p.seg_cost[p.n_seg];
   const int total = p.tile_off[p.n_seg];
   auto node_of = [&](int s) __attribute__((always_inline)) {
@@ -1756,6 +1774,10 @@ static int attention_launch(const void* q, long ldq, int q_rows_total, const int
              "attention: n_q=%d n_kv=%d needs a GQA group that is a multiple of 4", n_q, n_kv);
   QH_REQUIRE(n_seqs >= 0 && n_queries >= 0 && max_q >= 0, "attention: negative sizes");
   if (n_seqs == 0 || n_queries == 0) return QH_OK;
+  // the kernels index their workgroups (q-tile bound x head groups) in 32 bits
+  QH_REQUIRE(((long)n_queries / attn::BQ + n_seqs) * (n_q / attn::HPW) < (1L << 31),
+             "attention: %d queries in %d sequences x %d heads exceed 2^31 workgroups",
+             n_queries, n_seqs, n_q);
   const bool fp8 = out_q != nullptr;
   QH_REQUIRE(q && cu_q && kv_len && (fp8 ? out_scales != nullptr : out != nullptr),
              "attention: null pointer");
@@ -1956,6 +1978,10 @@ static int tree_attention_launch(const void* q, long ldq, int n_rows, const void
              n_q, n_kv);
   QH_REQUIRE(n_rows >= 0 && n_seg >= 0 && n_reads >= 0, "tree_attention: negative sizes");
   if (n_rows == 0 || n_seg == 0) return QH_OK;
+  // the streaming kernel indexes its workgroups (q-tile bound x head groups) in 32 bits
+  QH_REQUIRE(((long)n_rows / attn::BQ + n_seg) * (n_q / attn::HPW) < (1L << 31),
+             "tree_attention: %d rows in %d segments x %d heads exceed 2^31 workgroups",
+             n_rows, n_seg, n_q);
   const bool fp8 = out_q != nullptr;
   QH_REQUIRE(q && k_rows && v_rows && cu_a && seg_read && (fp8 ? scales != nullptr : out != nullptr),
              "tree_attention: null pointer");

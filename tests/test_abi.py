@@ -74,6 +74,14 @@ REJECTED = [
     ("qh_tree_attention", (None, 768, 1, None, None, 512, None, None, 1, None, None, 0, None, 0,
                            None, 0, 16, 6, 4, 128, 0.1, None, 0, None, 0, None, 0, None, 0,
                            None), "GQA group"),
+    # more workgroups than the kernels' 32-bit workgroup index covers (2^31 - 1 queries,
+    # 64 head groups)
+    ("qh_attention", (None, 0, 0, None, None, None, 0, None, 0, 16, None, None, 0, None, None,
+                      None, 1, (1 << 31) - 1, 1, 256, 64, 128, 0.1, 1, None, 0, None, 0, None,
+                      0, None), "exceed 2\\^31 workgroups"),
+    ("qh_tree_attention", (None, 32768, (1 << 31) - 1, None, None, 8192, None, None, 1, None,
+                           None, 0, None, 0, None, 0, 16, 256, 64, 128, 0.1, None, 0, None, 0,
+                           None, 0, None, 0, None), "exceed 2\\^31 workgroups"),
 ]
 
 
